@@ -98,8 +98,10 @@ def prefill_bench(case, steps, warmup, dev):
 
 
 def stage_bytes(cfg, T, n_distinct):
-    """Algorithmic HBM bytes per launch of each fused forward stage: weights
-    streamed once, plus activations in and out."""
+    """Algorithmic HBM bytes per launch of each decode stage (T <= 8): weights
+    streamed once, plus activations in and out.  "prep" = router logits +
+    quantized x; "up" = routing, routed + shared gate/up/SwiGLU and the
+    quantized mid rows; "dn" = routed down + slot sum + shared down."""
     d, I, E, Is, k = cfg.d_model, cfg.d_ff, cfg.n_expert, cfg.d_ff_shared, cfg.top_k
     iq2_row = (d // 256) * 66
     q2k_row = (I // 256) * 84
@@ -111,23 +113,39 @@ def stage_bytes(cfg, T, n_distinct):
         sh_up = sh_dn = 0
     return {
         "prep": E * d * 2 + T * d * 4 + T * E * 4 + T * (d // 256) * 292 + T * d * 9 // 8,
-        "up": n_distinct * 2 * I * iq2_row + sh_up + T * k * I * 4 + T * Is * 4,
-        "dn": n_distinct * d * q2k_row + sh_dn + T * k * (I // 256) * 292 + 2 * T * d * 4,
-        "decode": n_distinct * 2 * I * iq2_row + sh_up + n_distinct * d * q2k_row + sh_dn + E * d * 2 + T * d * 8,
+        "up": n_distinct * 2 * I * iq2_row + sh_up + T * k * I * 4 + T * k * (I // 256) * 292 + T * Is * 4
+              + T * Is * 9 // 8,
+        "dn": n_distinct * d * q2k_row + sh_dn + T * k * (I // 256) * 292 + T * Is * 9 // 8 + 2 * T * d * 4,
     }
 
 
 STAGE_KERNEL = {"prep": "dsmoe_prep", "select": "dsmoe_router_select", "up": "dsmoe_up_rows", "midq": "dsmoe_midq",
-                "dn": "dsmoe_dn_rows", "decode": "dsmoe_decode"}
+                "dn": "dsmoe_dn_rows"}
 
 
-def measured_traffic(kernel, config, path):
+def code_object_hash(kernel):
+    """First 16 hex digits of the SHA-256 of the code object holding `kernel`
+    (dsmoe_gemm.hsaco for the grouped GEMMs and the batch router, else
+    dsmoe_kernels.hsaco)."""
+    import hashlib
+    lib = os.path.join(ROOT, "deepseek-rs_amd", "lib")
+    gemm = kernel.startswith(("dsmoe_gu_grouped", "dsmoe_dn_grouped", "dsmoe_q80_gemm", "dsmoe_router_tile"))
+    f = os.path.join(lib, "dsmoe_gemm.hsaco" if gemm else "dsmoe_kernels.hsaco")
+    if not os.path.exists(f):
+        return None
+    return hashlib.sha256(open(f, "rb").read()).hexdigest()[:16]
+
+
+def measured_traffic(kernel, config, path, profiles=None):
     """HBM bytes per dispatch of `kernel` from the committed rocprofv3
-    FETCH_SIZE/WRITE_SIZE summaries (profiles/moe_decode_<config>_traffic.txt
-    and profiles/moe_prefill_<config>_traffic.txt, counters scaled by a copy
-    kernel of known size), or None when not measured."""
+    FETCH_SIZE/WRITE_SIZE summaries (profiles/moe_<decode|prefill>_<config>_traffic.txt,
+    counters scaled by a copy kernel of known size).  A summary line names
+    the code object it was measured on (code_object=<hash>); a line for
+    another build is stale and gives None, as does a kernel never measured."""
+    profiles = profiles or os.path.join(ROOT, "profiles")
+    want = code_object_hash(kernel)
     for kind in ("decode", "prefill"):
-        f = os.path.join(ROOT, "profiles", f"moe_{kind}_{config}_traffic.txt")
+        f = os.path.join(profiles, f"moe_{kind}_{config}_traffic.txt")
         if not os.path.exists(f):
             continue
         for line in open(f):
@@ -135,7 +153,7 @@ def measured_traffic(kernel, config, path):
                 continue
             kv = dict(t.split("=", 1) for t in line.split()[1:])
             if kv.get("kernel") == kernel and kv.get("config") == config and kv.get("path") == path:
-                return int(kv["bytes"])
+                return int(kv["bytes"]) if want and kv.get("code_object") == want else None
     return None
 
 
@@ -179,8 +197,6 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
-    ap.add_argument("--path", choices=["auto", "fused", "staged"], default="auto",
-                    help="decode path: one fused launch, or the staged launches (auto = library default)")
     ap.add_argument("--prefill-config", default="c5",
                     help="config of the prefill measurement added to the line ('none' to skip)")
     ap.add_argument("--prefill-steps", type=int, default=10)
@@ -204,9 +220,7 @@ def main():
     layers = [C.make_weights(case, layer=i, device=dev) for i in range(L)]
     xs = [C.make_x(case, T=T, step=s, device=dev) for s in range(16)]
     layer = dsmoe.MoeLayer(cfg, T)
-    if args.path != "auto":
-        layer.set_fused_decode(args.path == "fused")
-    path = "fused" if args.path == "fused" else "staged"
+    path = "staged"
     d, k = cfg.d_model, cfg.top_k
     so = torch.empty(T, d, device=dev)
     ro = torch.empty(T, d, device=dev)

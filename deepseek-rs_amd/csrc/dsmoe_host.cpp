@@ -80,18 +80,18 @@ const std::vector<uint8_t>& lvlmap_host() {
 // --------------------------------------------------------------------------
 // Code object + kernels, one set per device.
 // --------------------------------------------------------------------------
-enum Kern { K_PREP, K_ROUTER_SELECT, K_UP, K_MIDQ, K_DN, K_DECODE, K_SWIGLU, K_MOE_SUM, K_DISPATCH, K_SYNTH,
-            K_GU_GROUPED, K_DN_GROUPED, K_Q80_GEMM_SWIGLU, K_Q80_GEMM, K_UP_P, K_DN_P, K_STAGE_A, K_STAGE_B,
+enum Kern { K_PREP, K_ROUTER_SELECT, K_UP, K_MIDQ, K_DN, K_SWIGLU, K_MOE_SUM, K_DISPATCH, K_SYNTH,
+            K_GU_GROUPED, K_DN_GROUPED, K_Q80_GEMM_SWIGLU, K_Q80_GEMM,
             K_ROUTER_TILE, K_UP_ROWS, K_DN_ROWS, K_Q80_GEMM_SWIGLU_J7, K_Q80_GEMM_J7, K_Q80_GEMM_SWIGLU_J2,
             K_Q80_GEMM_J2, K_COUNT };
 const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_up", "dsmoe_midq", "dsmoe_dn",
-                                   "dsmoe_decode", "dsmoe_swiglu", "dsmoe_moe_sum", "dsmoe_dispatch", "dsmoe_synth",
+                                   "dsmoe_swiglu", "dsmoe_moe_sum", "dsmoe_dispatch", "dsmoe_synth",
                                    "dsmoe_gu_grouped", "dsmoe_dn_grouped", "dsmoe_q80_gemm_swiglu", "dsmoe_q80_gemm",
-                                   "dsmoe_up_p", "dsmoe_dn_p", "dsmoe_stage_a", "dsmoe_stage_b", "dsmoe_router_tile",
+                                   "dsmoe_router_tile",
                                    "dsmoe_up_rows", "dsmoe_dn_rows", "dsmoe_q80_gemm_swiglu_j7", "dsmoe_q80_gemm_j7",
                                    "dsmoe_q80_gemm_swiglu_j2", "dsmoe_q80_gemm_j2"};
 // code object of each kernel: 0 = dsmoe_kernels.hsaco, 1 = dsmoe_gemm.hsaco (same directory)
-const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0, 0, 1, 1, 1, 1};
+const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1};
 static_assert(DSMOE_GROUPED_TILE_M == kGuBM, "header and kernels disagree on the grouped tile");
 
 struct DeviceState {
@@ -165,9 +165,7 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // the workgroup (<= 1024 threads) and the grid has at least ~2 workgroups
 // per CU (256 CUs).
 constexpr int kMinWgs = 512;
-constexpr int kDecodeMaxT = kMaxDecodeT;  // dsmoe_decode handles up to 8 tokens
-constexpr uint32_t kSpinLimit = 1u << 22;  // ~seconds of polling before a wait gives up
-constexpr int kMaxTraceUnits = 16384;
+constexpr int kDecodeMaxT = kMaxDecodeT;  // row-streaming (matvec) launches up to 8 tokens, grouped GEMMs above
 
 int pow2_floor(int v) {
   int p = 1;
@@ -223,29 +221,6 @@ size_t q80_lds(int nb, int nmat, int R) { return (size_t)align_up(nb, 4) * 4 + (
 size_t select_lds(int E) { return (size_t)E * 16 + 64 * 24 + 32 * 4; }
 size_t router_lds(int) { return 8 * 256 * 4; }
 
-// Word layout of the decode launch's hand-off area (see DecodeArgs).
-struct SyncMap {
-  int flags, tr_q8k, tr_q80, tr_router, tr_tokmid, tr_tokmid_stride, tr_sh, tr_sh_stride, midrows, shrows, total;
-};
-SyncMap sync_map(const dsmoe_config& cf) {
-  const int T = kMaxDecodeT, K = cf.top_k, d = cf.d_model, nbI = cf.d_ff / 256;
-  const int ngsh = std::max(1, (cf.d_ff_shared + 255) / 256);
-  SyncMap m{};
-  int at = 32;
-  m.flags = at;                 at += kNumFlags * kFlagWords;
-  m.tr_q8k = at;                at += tree_words((d / 256) * T);
-  m.tr_q80 = at;                at += tree_words(((d / 32 + 7) / 8) * T);
-  m.tr_router = at;             at += tree_words(cf.n_expert * ((T + 7) / 8));
-  m.tr_tokmid_stride = tree_words(K * nbI);
-  m.tr_tokmid = at;             at += T * m.tr_tokmid_stride;
-  m.tr_sh_stride = tree_words(ngsh);
-  m.tr_sh = at;                 at += T * m.tr_sh_stride;
-  m.midrows = at;               at += T * K * nbI;
-  m.shrows = at;                at += T * ngsh;
-  m.total = at;
-  return m;
-}
-
 int validate_cfg(const dsmoe_config* c) {
   if (!c) return fail(DSMOE_ERR_INVALID, "config is NULL");
   if (c->d_model <= 0 || c->d_model % 512 || c->d_model > 8192)
@@ -279,7 +254,7 @@ int validate_cfg(const dsmoe_config* c) {
 // ==========================================================================
 extern "C" {
 
-const char* dsmoe_version(void) { return "dsmoe 0.1 (gfx950)"; }
+const char* dsmoe_version(void) { return "dsmoe 0.2 (gfx950)"; }
 const char* dsmoe_last_error(void) { return g_err.c_str(); }
 
 int dsmoe_init(const char* code_object_path) {
@@ -393,19 +368,19 @@ int dsmoe_q8_0_quantize(const float* x, int8_t* xq, float* xscale, int32_t in_di
 // Shapes + argument blocks of the matvec roles (validated by the callers).
 static GateUpArgs gate_up_args(const void* gate, const void* up, const void* xq, const int32_t* selected,
                                const float* weights, const uint32_t* pair_list, float* gate_out, float* up_out,
-                               float* mid_out, int d, int I, int k, float clamp, int n_work, Shape* sh,
+                               float* mid_out, int d, int I, int k, int E, float clamp, int n_work, Shape* sh,
                                int max_block = 512) {
   const int nbp = d / 512;
   *sh = matvec_shape(2 * nbp, 16, I, n_work, max_block);
   return GateUpArgs{(const uint8_t*)gate, (const uint8_t*)up, (const uint8_t*)xq, selected, weights, pair_list,
-                    gate_out, up_out, mid_out, d, I, k, sh->R, clamp};
+                    gate_out, up_out, mid_out, d, I, k, sh->R, E, clamp};
 }
 
 static DownArgs down_args(const void* down, const void* midq, const int32_t* selected, float* down_out, float* out,
-                          int d, int I, int k, int T, Shape* sh, int max_block = 1024) {
+                          int d, int I, int k, int E, int T, Shape* sh, int max_block = 1024) {
   const int nb = I / 256;
   *sh = matvec_shape(k * nb, 8 * k, d, T, max_block);
-  return DownArgs{(const uint8_t*)down, (const uint8_t*)midq, selected, out, down_out, d, I, k, sh->R};
+  return DownArgs{(const uint8_t*)down, (const uint8_t*)midq, selected, out, down_out, d, I, k, sh->R, E};
 }
 
 static Q80MatvecArgs q80_args(const void* w0, const void* w1, const int8_t* xq, const float* xs, float* out0,
@@ -443,12 +418,13 @@ static int check_q80(const void* w0, const void* w1, const int8_t* xq, const flo
 
 int dsmoe_gate_up_mid(const void* gate, const void* up, const void* xq, const int32_t* selected,
                       const float* weights, float* gate_out, float* up_out, float* mid_out, int32_t d,
-                      int32_t I, int32_t T, int32_t k, float clamp, dsmoe_stream_t stream) {
+                      int32_t I, int32_t T, int32_t k, int32_t E, float clamp, dsmoe_stream_t stream) {
   if (T < 0) return fail(DSMOE_ERR_INVALID, "gate_up_mid: T < 0");
+  if (E < 1) return fail(DSMOE_ERR_INVALID, "gate_up_mid: E < 1");
   DSM_TRY(check_gate_up(gate, up, xq, mid_out, d, I, k));
   UpArgs a{};
   Shape sh;
-  a.gu = gate_up_args(gate, up, xq, selected, weights, nullptr, gate_out, up_out, mid_out, d, I, k, clamp, T * k, &sh);
+  a.gu = gate_up_args(gate, up, xq, selected, weights, nullptr, gate_out, up_out, mid_out, d, I, k, E, clamp, T * k, &sh);
   a.gu_work = T * k;
   if (up_rows_fits(d)) {
     a.gu_tiles = (I + kUpRowsR - 1) / kUpRowsR;
@@ -459,13 +435,14 @@ int dsmoe_gate_up_mid(const void* gate, const void* up, const void* xq, const in
 }
 
 int dsmoe_down(const void* down, const void* midq, const int32_t* selected, float* down_out, float* out,
-               int32_t d, int32_t I, int32_t T, int32_t k, dsmoe_stream_t stream) {
+               int32_t d, int32_t I, int32_t T, int32_t k, int32_t E, dsmoe_stream_t stream) {
   if (!down_out && !out) return fail(DSMOE_ERR_INVALID, "down: null pointer");
   if (T < 0) return fail(DSMOE_ERR_INVALID, "down: bad shape");
+  if (E < 1) return fail(DSMOE_ERR_INVALID, "down: E < 1");
   DSM_TRY(check_down(down, midq, d, I, k));
   DnArgs a{};
   Shape sh;
-  a.dn = down_args(down, midq, selected, down_out, out, d, I, k, T, &sh);
+  a.dn = down_args(down, midq, selected, down_out, out, d, I, k, E, T, &sh);
   a.dn_work = T;
   if (dn_rows_fits(I, k)) {
     a.dn_tiles = (d + kDnRowsR - 1) / kDnRowsR;
@@ -614,27 +591,11 @@ struct dsmoe_ctx {
   uint32_t* g_tile_offsets = nullptr;
   uint32_t* g_tile_experts = nullptr;
   uint32_t* g_tile_starts = nullptr;
-  uint32_t* sync = nullptr;  // dsmoe_decode counters (zero between launches)
-  uint32_t* sync3 = nullptr;  // three-launch decode: router tree | mid row counters (zero between launches)
-  bool three_stage = false;   // DSMOE_OPT_THREE_STAGE
-  int interleave = 0;         // DSMOE_OPT_INTERLEAVE: bits 0/2 gate/up launch, bits 1/3 down launch
-  int block_up = 0;           // DSMOE_OPT_BLOCK_UP: 0 = row-streaming gate/up launch, else per-item with that block
-  int block_dn = 0;           // DSMOE_OPT_BLOCK_DN: 0 = row-streaming down launch, else per-item with that block
-  bool fuse_midq = true;      // DSMOE_OPT_FUSE_MIDQ: mid quantization inside the row-streaming gate/up launch
-  int32_t n_sync = 0;
-  // per-stage timing
+  // mid row counters of the fused mid quantization in dsmoe_up_rows:
+  // [kMaxDecodeT*k*(I/256)] routed, then [kMaxDecodeT*ceil(I_s/256)] shared;
+  // zero between launches (the workgroup completing a block resets its word)
+  uint32_t* mid_cnt = nullptr;
   bool profiling = false;
-  bool fused_decode = false;  // DSMOE_OPT_FUSED_DECODE
-  bool persistent = false;     // DSMOE_OPT_PERSISTENT_STAGES
-  std::map<std::pair<int, size_t>, int> occ;  // (kernel, LDS bytes) -> resident workgroups
-  int wgs_per_cu = 0;          // DSMOE_OPT_DECODE_WGS_PER_CU
-  int poll_sleep = 2;          // DSMOE_OPT_POLL_SLEEP
-  int hold_streams = 0;        // DSMOE_OPT_HOLD_STREAMS
-  size_t occ_lds = ~(size_t)0;  // dsmoe_decode occupancy, cached per LDS size
-  int occ_blocks = 0;
-  int occ_cus = 0;
-  uint64_t* trace = nullptr;  // dsmoe_set_trace
-  uint32_t epoch = 0;         // decode launches so far (flag value of the next one)
   std::vector<hipEvent_t> event_pool;
   std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> pending;
   double stage_ms[DSMOE_STAGE_COUNT] = {};
@@ -642,25 +603,6 @@ struct dsmoe_ctx {
 };
 
 namespace {
-// Workgroups of kernel k (256 threads, `lds` dynamic bytes) the GPU holds at
-// once, capped by `units`: the grid of a persistent launch.
-int persistent_grid(dsmoe_ctx* c, Kern k, size_t lds, int units, int* grid) {
-  const auto key = std::make_pair((int)k, lds);
-  auto it = c->occ.find(key);
-  if (it == c->occ.end()) {
-    DeviceState* st = nullptr;
-    DSM_TRY(load_device(nullptr, &st));
-    int per_cu = 0, dev = 0, cus = 0;
-    DSM_CHECK_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, st->fn[k], 256, lds));
-    DSM_CHECK_HIP(hipGetDevice(&dev));
-    DSM_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    if (per_cu < 1) return fail(DSMOE_ERR_UNSUPPORTED, "persistent launch does not fit a compute unit");
-    it = c->occ.emplace(key, per_cu * cus).first;
-  }
-  *grid = std::max(1, std::min(it->second, units));
-  return DSMOE_OK;
-}
-
 template <class T>
 int ctx_alloc(dsmoe_ctx* c, T** p, size_t bytes) {
   void* q = nullptr;
@@ -706,42 +648,9 @@ struct StageScope {
 extern "C" {
 
 const char* dsmoe_stage_name(int32_t stage) {
-  static const char* names[DSMOE_STAGE_COUNT] = {"prep", "select", "up", "midq", "dn", "decode",
+  static const char* names[DSMOE_STAGE_COUNT] = {"prep", "select", "up", "midq", "dn",
                                                  "gu_grouped", "shared_up", "dn_grouped", "shared_dn"};
   return (stage >= 0 && stage < DSMOE_STAGE_COUNT) ? names[stage] : "?";
-}
-
-int dsmoe_set_option(dsmoe_ctx* c, int32_t option, int32_t value) {
-  if (!c) return fail(DSMOE_ERR_INVALID, "set_option: ctx is NULL");
-  if (option == DSMOE_OPT_FUSED_DECODE) { c->fused_decode = value != 0; return DSMOE_OK; }
-  if (option == DSMOE_OPT_PERSISTENT_STAGES) { c->persistent = value != 0; return DSMOE_OK; }
-  if (option == DSMOE_OPT_HOLD_STREAMS) { c->hold_streams = value != 0; return DSMOE_OK; }
-  if (option == DSMOE_OPT_THREE_STAGE) { c->three_stage = value != 0; return DSMOE_OK; }
-  if (option == DSMOE_OPT_INTERLEAVE) { c->interleave = value & 15; return DSMOE_OK; }
-  if (option == DSMOE_OPT_FUSE_MIDQ) { c->fuse_midq = value != 0; return DSMOE_OK; }
-  if (option == DSMOE_OPT_BLOCK_UP || option == DSMOE_OPT_BLOCK_DN) {
-    if (value != 0 && value != 256 && value != 512 && value != 1024)
-      return fail(DSMOE_ERR_INVALID, "set_option: block must be 0, 256, 512 or 1024");
-    (option == DSMOE_OPT_BLOCK_UP ? c->block_up : c->block_dn) = value;
-    return DSMOE_OK;
-  }
-  if (option == DSMOE_OPT_POLL_SLEEP) {
-    if (value < 0 || value > 1000) return fail(DSMOE_ERR_INVALID, "set_option: poll sleep outside 0..1000");
-    c->poll_sleep = value;
-    return DSMOE_OK;
-  }
-  if (option == DSMOE_OPT_DECODE_WGS_PER_CU) {
-    if (value < 0) return fail(DSMOE_ERR_INVALID, "set_option: negative workgroups per CU");
-    c->wgs_per_cu = value;
-    return DSMOE_OK;
-  }
-  return fail(DSMOE_ERR_INVALID, "set_option: unknown option");
-}
-
-int dsmoe_set_trace(dsmoe_ctx* c, void* buf) {
-  if (!c) return fail(DSMOE_ERR_INVALID, "set_trace: ctx is NULL");
-  c->trace = (uint64_t*)buf;
-  return DSMOE_OK;
 }
 
 int dsmoe_set_profiling(dsmoe_ctx* c, int32_t enable) {
@@ -815,22 +724,10 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
     A(&c->g_tile_starts, max_tiles * 4);
   }
   {
-    // router tree | mid row counters (routed, then the shared groups of the
-    // fused quantization in the row-streaming gate/up launch)
-    const size_t words = tree_words((int)E * ((kMaxDecodeT + 7) / 8)) + (size_t)kMaxDecodeT * K * (I / 256) +
-                         (size_t)kMaxDecodeT * ((Is + 255) / 256);
-    A(&c->sync3, words * 4);
-    if (rc == DSMOE_OK && hipMemset(c->sync3, 0, words * 4) != hipSuccess)
-      rc = fail(DSMOE_ERR_HIP, "create: hipMemset of the stage counters failed");
-  }
-  {
-    const int Td = kMaxDecodeT, P = Td * (int)K, nbI = (int)(I / 256), ng = (int)((Is + 255) / 256);
-    SyncMap m = sync_map(*cfg);
-    c->n_sync = m.total;
-    (void)P; (void)nbI; (void)ng; (void)Td;
-    A(&c->sync, (size_t)c->n_sync * 4);
-    if (rc == DSMOE_OK && hipMemset(c->sync, 0, (size_t)c->n_sync * 4) != hipSuccess)
-      rc = fail(DSMOE_ERR_HIP, "create: hipMemset of the sync words failed");
+    const size_t words = (size_t)kMaxDecodeT * K * (I / 256) + (size_t)kMaxDecodeT * ((Is + 255) / 256);
+    A(&c->mid_cnt, words * 4);
+    if (rc == DSMOE_OK && hipMemset(c->mid_cnt, 0, words * 4) != hipSuccess)
+      rc = fail(DSMOE_ERR_HIP, "create: hipMemset of the mid row counters failed");
   }
   if (rc != DSMOE_OK) {
     std::string msg = g_err;
@@ -856,178 +753,6 @@ int dsmoe_destroy(dsmoe_ctx* c) {
 
 size_t dsmoe_scratch_bytes(const dsmoe_ctx* c) { return c ? c->bytes : 0; }
 
-int dsmoe_check(dsmoe_ctx* c, dsmoe_stream_t stream) {
-  if (!c) return fail(DSMOE_ERR_INVALID, "check: ctx is NULL");
-  uint32_t err = 0;
-  DSM_CHECK_HIP(hipMemcpyAsync(&err, c->sync + kSyncErr, 4, hipMemcpyDeviceToHost, (hipStream_t)stream));
-  DSM_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
-  if (err) {
-    // an abandoned launch can leave counters half-counted: start over from zero
-    DSM_CHECK_HIP(hipMemsetAsync(c->sync, 0, (size_t)c->n_sync * 4, (hipStream_t)stream));
-    DSM_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
-    c->epoch = 0;
-    return fail(DSMOE_ERR_SYNC, "check: a device-side dependency wait timed out; outputs since the last check are invalid");
-  }
-  return DSMOE_OK;
-}
-
-// The whole layer for T <= kDecodeMaxT tokens as one persistent launch
-// (dsmoe_decode); same arithmetic and outputs as the staged path below.
-static int forward_decode(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int T, float* shared_out,
-                          float* routed_out, int32_t* sel, float* wts, dsmoe_stream_t stream) {
-  const dsmoe_config& cf = c->cfg;
-  const int d = cf.d_model, I = cf.d_ff, K = cf.top_k, Is = cf.d_ff_shared, E = cf.n_expert;
-  const int nb = d / 256, P = T * K, B = 256;
-  DecodeArgs a{};
-  a.router = RouterLogitsArgs{(const uint16_t*)w->router_f16, x, c->logits, d, E, T};
-  a.q8k = Q8KArgs{x, c->xq8k, d, T};
-  a.q80 = Q80Args{x, c->xq80, c->xs80, d, T};
-  a.sel = RouterSelectArgs{c->logits, cf.has_bias ? w->bias : nullptr, nullptr, sel, wts, T, E, K,
-                           cf.n_group > 1 ? cf.n_group : 1, cf.topk_group, cf.has_bias ? 1 : 0, cf.route_scale};
-  Shape sgu, ssu{0, 0, 0}, ssd{0, 0, 0}, sdn;
-  a.gu = gate_up_args(w->gate, w->up, c->xq8k, sel, wts, nullptr, nullptr, nullptr, c->mid, d, I, K, cf.swiglu_clamp, P,
-                      &sgu, B);
-  a.midq = Q8KArgs{c->mid, c->midq, I, P};
-  a.dn = down_args(w->down, c->midq, sel, nullptr, routed_out, d, I, K, T, &sdn, B);
-  size_t lds = std::max<size_t>(router_lds(d), select_lds(E));
-  lds = std::max(lds, gate_up_lds(nb, sgu.R));
-  lds = std::max(lds, down_lds(K, I / 256, sdn.R));
-  a.sh_fmt = cf.shared_fmt;
-  if (cf.shared_fmt == 0) {
-    a.sh_q80 = q80_args(w->sh_gate, w->sh_up, c->xq80, c->xs80, nullptr, nullptr, c->sh_mid, d, Is, T, cf.swiglu_clamp,
-                        &ssu, B);
-    a.sh_midq80 = Q80Args{c->sh_mid, c->sh_q80, c->sh_s80, Is, T};
-    a.sh_dn = q80_args(w->sh_down, nullptr, c->sh_q80, c->sh_s80, shared_out, nullptr, nullptr, Is, d, T, 0.0f, &ssd, B);
-    lds = std::max(lds, q80_lds(d / 32, 2, ssu.R));
-    lds = std::max(lds, q80_lds(Is / 32, 1, ssd.R));
-  } else if (cf.shared_fmt == 1) {
-    a.sh_iq2 = gate_up_args(w->sh_gate, w->sh_up, c->xq8k, nullptr, nullptr, nullptr, nullptr, nullptr, c->sh_mid, d, Is,
-                            1, cf.swiglu_clamp, T, &ssu, B);
-    a.sh_midq8k = Q8KArgs{c->sh_mid, c->sh_midq, Is, T};
-    a.sh_q2k = down_args(w->sh_down, c->sh_midq, nullptr, nullptr, shared_out, d, Is, 1, T, &ssd, B);
-    lds = std::max(lds, gate_up_lds(nb, ssu.R));
-    lds = std::max(lds, down_lds(1, Is / 256, ssd.R));
-  }
-  a.sync = c->sync;
-  a.T = T;
-  a.K = K;
-  a.n_q8k = nb * T;
-  a.n_q80 = cf.shared_fmt == 0 ? ((d / 32 + 7) / 8) * T : 0;
-  a.n_router = E * ((T + 7) / 8);
-  a.shup_tiles = ssu.tiles;
-  a.n_shup = cf.shared_fmt >= 0 ? ssu.tiles * T : 0;
-  a.gu_tiles = sgu.tiles;
-  a.n_gu = sgu.tiles * P;
-  a.shdn_tiles = ssd.tiles;
-  a.n_shdn = cf.shared_fmt >= 0 ? ssd.tiles * T : 0;
-  a.dn_tiles = sdn.tiles;
-  a.n_dn = sdn.tiles * T;
-  const SyncMap m = sync_map(cf);
-  a.flags = m.flags;
-  a.tr_q8k = m.tr_q8k;
-  a.tr_q80 = m.tr_q80;
-  a.tr_router = m.tr_router;
-  a.tr_tokmid = m.tr_tokmid;
-  a.tr_tokmid_stride = m.tr_tokmid_stride;
-  a.tr_sh = m.tr_sh;
-  a.tr_sh_stride = m.tr_sh_stride;
-  a.midrows = m.midrows;
-  a.shrows = m.shrows;
-  a.epoch = ++c->epoch;
-  if (a.epoch == 0) a.epoch = ++c->epoch;  // 0 is the flags' initial value
-  a.spin_limit = kSpinLimit;
-  a.poll_sleep = (uint32_t)c->poll_sleep;
-  a.hold_streams = c->hold_streams;
-  a.trace = c->trace;
-  const int units = a.n_q8k + a.n_q80 + a.n_router + a.n_shup + a.n_gu + a.n_shdn + a.n_dn;
-  if (c->trace && units > kMaxTraceUnits) return fail(DSMOE_ERR_UNSUPPORTED, "trace: more work units than the trace holds");
-  // persistent grid: every workgroup the GPU holds at once (all must be resident)
-  if (lds != c->occ_lds) {
-    DeviceState* st = nullptr;
-    DSM_TRY(load_device(nullptr, &st));
-    int per_cu = 0, dev = 0, cus = 0;
-    DSM_CHECK_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, st->fn[K_DECODE], B, lds));
-    DSM_CHECK_HIP(hipGetDevice(&dev));
-    DSM_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    if (per_cu < 1) return fail(DSMOE_ERR_UNSUPPORTED, "decode: kernel does not fit a compute unit");
-    c->occ_lds = lds;
-    c->occ_blocks = per_cu * cus;
-    c->occ_cus = cus;
-  }
-  int grid = c->occ_blocks;
-  if (c->wgs_per_cu > 0) grid = std::min(grid, c->wgs_per_cu * c->occ_cus);
-  grid = std::min(grid, units);
-  StageScope sc(c, DSMOE_STAGE_DECODE, stream);
-  return launch(K_DECODE, dim3(grid), dim3(B), lds, stream, a);
-}
-
-// Decode in three launches (T <= 8, Q8_0 or no shared expert).
-static int forward_three(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int T, float* shared_out,
-                         float* routed_out, int32_t* sel, float* wts, dsmoe_stream_t stream) {
-  const dsmoe_config& cf = c->cfg;
-  const int d = cf.d_model, I = cf.d_ff, K = cf.top_k, Is = cf.d_ff_shared, E = cf.n_expert, nb = d / 256;
-  const int P = T * K, B = 256;
-  const bool sh = cf.shared_fmt == 0;
-  // A. router rows (+ selection by the last) + Q8_K(x) + shared gate/up  (session.rs:1894-1959, 1989-2073)
-  {
-    StageScope sc(c, DSMOE_STAGE_PREP, stream);
-    StageAArgs a{};
-    a.router = RouterLogitsArgs{(const uint16_t*)w->router_f16, x, c->logits, d, E, T};
-    a.sel = RouterSelectArgs{c->logits, cf.has_bias ? w->bias : nullptr, nullptr, sel, wts, T, E, K,
-                             cf.n_group > 1 ? cf.n_group : 1, cf.topk_group, cf.has_bias ? 1 : 0, cf.route_scale};
-    a.q8k = Q8KArgs{x, c->xq8k, d, T};
-    a.x = x;
-    a.sync = c->sync3;
-    a.n_router = E * ((T + 7) / 8);
-    a.n_q8k = nb * T;
-    size_t lds = std::max(router_lds(d), select_lds(E));
-    lds = std::max<size_t>(lds, 2 * 256 * 4 + 256);
-    if (sh) {
-      Shape s;
-      a.sh_q80 = q80_args(w->sh_gate, w->sh_up, nullptr, nullptr, nullptr, nullptr, c->sh_mid, d, Is, T,
-                          cf.swiglu_clamp, &s, B);
-      a.shup_tiles = s.tiles;
-      a.n_shup = s.tiles * T;
-      lds = std::max(lds, q80_lds(d / 32, 2, s.R));
-    }
-    DSM_TRY(launch(K_STAGE_A, dim3(a.n_router + a.n_q8k + a.n_shup), dim3(B), lds, stream, a));
-  }
-  // B. routed gate/up (+ Q8_K of each completed 256-row block) + shared down  (session.rs:1960-1987, 2075-2127)
-  {
-    StageScope sc(c, DSMOE_STAGE_UP, stream);
-    StageBArgs a{};
-    Shape s1;
-    a.gu = gate_up_args(w->gate, w->up, c->xq8k, sel, wts, nullptr, nullptr, nullptr, c->mid, d, I, K,
-                        cf.swiglu_clamp, P, &s1, B);
-    a.gu_tiles = s1.tiles;
-    a.n_gu = s1.tiles * P;
-    a.midq = Q8KArgs{c->mid, c->midq, I, P};
-    a.sh_mid = c->sh_mid;
-    a.sync = c->sync3 + tree_words(E * ((kMaxDecodeT + 7) / 8));
-    size_t lds = std::max<size_t>(gate_up_lds(nb, s1.R), 2 * 256 * 4 + 256);
-    if (sh) {
-      Shape s2;
-      a.sh_dn = q80_args(w->sh_down, nullptr, nullptr, nullptr, shared_out, nullptr, nullptr, Is, d, T, 0.0f, &s2, B);
-      a.shdn_tiles = s2.tiles;
-      a.n_shdn = s2.tiles * T;
-      lds = std::max(lds, q80_lds(Is / 32, 1, s2.R));
-    }
-    DSM_TRY(launch(K_STAGE_B, dim3(a.n_gu + a.n_shdn), dim3(B), lds, stream, a));
-  }
-  // C. routed down + slot sum  (session.rs:1977-1986, 2129-2153)
-  {
-    StageScope sc(c, DSMOE_STAGE_DN, stream);
-    DnArgs a{};
-    Shape s1;
-    a.dn = down_args(w->down, c->midq, sel, nullptr, routed_out, d, I, K, T, &s1);
-    a.dn_tiles = s1.tiles;
-    a.dn_work = T;
-    a.sh_fmt = -1;
-    DSM_TRY(launch(K_DN, dim3(a.dn_tiles * a.dn_work), dim3(s1.block), down_lds(K, I / 256, s1.R), stream, a));
-  }
-  return DSMOE_OK;
-}
-
 int dsmoe_forward(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t T, float* shared_out,
                   float* routed_out, int32_t* selected, float* weights, dsmoe_stream_t stream) {
   if (!c || !w || !x || !routed_out) return fail(DSMOE_ERR_INVALID, "forward: null pointer");
@@ -1038,30 +763,26 @@ int dsmoe_forward(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t 
   if (cf.shared_fmt >= 0 && (!w->sh_gate || !w->sh_up || !w->sh_down || !shared_out))
     return fail(DSMOE_ERR_INVALID, "forward: missing shared expert weights or output");
   if (T == 0) return DSMOE_OK;
-  const int d = cf.d_model, I = cf.d_ff, K = cf.top_k, Is = cf.d_ff_shared;
+  const int d = cf.d_model, I = cf.d_ff, K = cf.top_k, Is = cf.d_ff_shared, E = cf.n_expert;
   int32_t* sel = selected ? selected : c->selected;
   float* wts = weights ? weights : c->weights;
-
-  const int nb = d / 256;
-  if (T <= kDecodeMaxT && c->fused_decode) return forward_decode(c, w, x, T, shared_out, routed_out, sel, wts, stream);
-  if (T <= kDecodeMaxT && c->three_stage && cf.shared_fmt != 1)
-    return forward_three(c, w, x, T, shared_out, routed_out, sel, wts, stream);
-  // batches: routed experts as grouped GEMMs over pairs sorted by expert
+  const int nb = d / 256, P = T * K;
+  // Batches (T > 8, E <= 512: the dispatch sort's limit) run the routed
+  // experts as grouped GEMMs over pairs sorted by expert; everything else
+  // runs the matvec launches, one work item per (row tile, pair / token).
   const bool grouped = T > kDecodeMaxT && c->xh != nullptr;
-  const int E = cf.n_expert, P = T * K;
   // 1. router logits + Q8_K(x) + Q8_0(x)          (session.rs:1894-1909, 1991-2008, 2062-2073)
   {
     StageScope sc(c, DSMOE_STAGE_PREP, stream);
-    RouterLogitsArgs r{(const uint16_t*)w->router_f16, x, c->logits, d, cf.n_expert, T};
+    RouterLogitsArgs r{(const uint16_t*)w->router_f16, x, c->logits, d, E, T};
     Q8KArgs q8k{x, c->xq8k, d, T, grouped ? c->xh : nullptr};
     Q80Args q80{x, c->xq80, c->xs80, d, T, grouped ? c->xh80 : nullptr};
     DSM_TRY(prep_impl(&r, &q8k, cf.shared_fmt == 0 ? &q80 : nullptr, stream));
   }
   // 2. routing                                     (session.rs:2010-2058)
-  // In the row-streaming decode path every routed gate/up workgroup runs the
+  // In the row-streaming path every routed gate/up workgroup runs the
   // one-wave selection itself (no launch of its own).
-  const bool up_rows = !grouped && !c->persistent && c->block_up == 0 && up_rows_fits(d) &&
-                       (cf.shared_fmt != 0 || q80_rows_fits(d));
+  const bool up_rows = !grouped && up_rows_fits(d) && (cf.shared_fmt != 0 || q80_rows_fits(d));
   const int fuse_p = up_rows ? select_wave_p(cf) : 0;
   if (!fuse_p) {
     StageScope sc(c, DSMOE_STAGE_SELECT, stream);
@@ -1072,28 +793,25 @@ int dsmoe_forward(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t 
   }
   // 3. routed + shared gate/up/SwiGLU              (session.rs:1910-1959, 2075-2112)
   // The row-streaming launch also quantizes the mid rows (step 4) when the
-  // shared expert is Q8_0 or absent.
-  const bool fuse_midq = up_rows && c->fuse_midq && (cf.shared_fmt == -1 || (cf.shared_fmt == 0 && cf.d_ff_shared % 32 == 0));
+  // shared expert is Q8_0 or absent; its row counters cover kDecodeMaxT tokens.
+  const bool fuse_midq = up_rows && T <= kDecodeMaxT &&
+                         (cf.shared_fmt == -1 || (cf.shared_fmt == 0 && Is % 32 == 0));
   {
     StageScope sc(c, DSMOE_STAGE_UP, stream);
     UpArgs a{};
     Shape s1, s2{0, 64, 0};
-    const bool pers = !grouped && c->persistent;  // one item per thread per unit: 256-thread shapes
-    // row-streaming launch (default) or per-item launch (an explicit DSMOE_OPT_BLOCK_UP)
-    const bool rows = up_rows;
-    const int mb = (pers || rows) ? 256 : (c->block_up ? c->block_up : 256);
+    const int mb = 256;
     if (fuse_p) {
       a.fuse_sel = fuse_p;
-      a.sel = RouterSelectArgs{c->logits, cf.has_bias ? w->bias : nullptr, nullptr, sel, wts, T, cf.n_expert,
-                               cf.top_k, cf.n_group > 1 ? cf.n_group : 1, cf.topk_group, cf.has_bias ? 1 : 0,
-                               cf.route_scale};
+      a.sel = RouterSelectArgs{c->logits, cf.has_bias ? w->bias : nullptr, nullptr, sel, wts, T, E, K,
+                               cf.n_group > 1 ? cf.n_group : 1, cf.topk_group, cf.has_bias ? 1 : 0, cf.route_scale};
     }
-    a.gu = gate_up_args(w->gate, w->up, c->xq8k, sel, wts, nullptr, nullptr, nullptr, c->mid, d, I, K,
-                        cf.swiglu_clamp, T * K, &s1, mb);
-    if (rows) { s1.R = kUpRowsR; s1.block = 256; s1.tiles = (I + kUpRowsR - 1) / kUpRowsR; }
+    a.gu = gate_up_args(w->gate, w->up, c->xq8k, sel, wts, nullptr, nullptr, nullptr, c->mid, d, I, K, E,
+                        cf.swiglu_clamp, P, &s1, mb);
+    if (up_rows) { s1.R = kUpRowsR; s1.block = 256; s1.tiles = (I + kUpRowsR - 1) / kUpRowsR; }
     a.gu_tiles = s1.tiles;
-    a.gu_work = grouped ? 0 : T * K;
-    size_t lds = rows ? gate_up_rows_lds(nb) : gate_up_lds(nb, s1.R);
+    a.gu_work = grouped ? 0 : P;
+    size_t lds = up_rows ? gate_up_rows_lds(nb) : gate_up_lds(nb, s1.R);
     if (grouped) {
       StageScope sg(c, DSMOE_STAGE_GU_GROUPED, stream);
       DSM_TRY(dsmoe_gate_up_mid_sorted(w->gate, w->up, c->xh, c->xq8k, c->g_sorted, c->g_offsets, c->g_tile_offsets,
@@ -1107,11 +825,11 @@ int dsmoe_forward(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t 
       lds = std::max(lds, q80_lds(d / 32, 2, s2.R));
     } else if (cf.shared_fmt == 1) {
       a.sh_iq2 = gate_up_args(w->sh_gate, w->sh_up, c->xq8k, nullptr, nullptr, nullptr, nullptr, nullptr, c->sh_mid,
-                              d, Is, 1, cf.swiglu_clamp, T, &s2, mb);
+                              d, Is, 1, 1, cf.swiglu_clamp, T, &s2, mb);
       lds = std::max(lds, gate_up_lds(nb, s2.R));
     }
     if (cf.shared_fmt >= 0) { a.sh_tiles = s2.tiles; a.sh_work = T; }
-    if (rows && cf.shared_fmt == 0) {  // Q8_0 row-streaming tiles: 4 rows of gate and of up
+    if (up_rows && cf.shared_fmt == 0) {  // Q8_0 row-streaming tiles: 4 rows of gate and of up
       a.sh_tiles = q80_rows_tiles(Is, true);
       lds = std::max(lds, q80_rows_lds(d / 32));
     }
@@ -1120,30 +838,20 @@ int dsmoe_forward(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t 
       StageScope sg(c, DSMOE_STAGE_SH_UP, stream);
       DSM_TRY(dsmoe_q8_0_gemm(w->sh_gate, w->sh_up, c->xh80, c->xs80, c->sh_mid, d, Is, T, cf.swiglu_clamp, stream));
     }
-    const int units = a.gu_tiles * a.gu_work + a.sh_tiles * a.sh_work;
-    if (pers) {  // the Q8_0 shared layout sits above the gate/up layout (both stay staged)
-      a.sh_lds_offset = align_up((int)gate_up_lds(nb, s1.R), 16);
-      if (cf.shared_fmt == 0) lds = a.sh_lds_offset + q80_lds(d / 32, 2, s2.R);
-      int grid = 0;
-      DSM_TRY(persistent_grid(c, K_UP_P, lds, units, &grid));
-      a.trace = c->trace;
-      DSM_TRY(launch(K_UP_P, dim3(grid), dim3(256), lds, stream, a));
-    } else {
-      a.interleave = (c->interleave & 4) ? 2 : (c->interleave & 1);
-      a.trace = c->trace;
-      if (fuse_midq) {
-        a.fuse_midq = 1;
-        a.midq = Q8KArgs{c->mid, c->midq, I, T * K};
-        a.sh_midq = Q80Args{c->sh_mid, c->sh_q80, c->sh_s80, Is, T};
-        a.mid_cnt = c->sync3 + tree_words(E * ((kMaxDecodeT + 7) / 8));
-      }
-      DSM_TRY(launch(rows ? K_UP_ROWS : K_UP, dim3(units), dim3(rows ? 256 : std::max(s1.block, s2.block)), lds, stream, a));
+    if (fuse_midq) {
+      a.fuse_midq = 1;
+      a.midq = Q8KArgs{c->mid, c->midq, I, P};
+      a.sh_midq = Q80Args{c->sh_mid, c->sh_q80, c->sh_s80, Is, T};
+      a.mid_cnt = c->mid_cnt;
     }
+    const int units = a.gu_tiles * a.gu_work + a.sh_tiles * a.sh_work;
+    DSM_TRY(launch(up_rows ? K_UP_ROWS : K_UP, dim3(units), dim3(up_rows ? 256 : std::max(s1.block, s2.block)), lds,
+                   stream, a));
   }
   // 4. Q8_K(mid) + Q8_0 / Q8_K of the shared mid  (session.rs:1964-1976, 2114-2127)
   if (!fuse_midq) {
     StageScope sc(c, DSMOE_STAGE_MIDQ, stream);
-    Q8KArgs qa{c->mid, c->midq, I, T * K, grouped ? c->mh : nullptr};
+    Q8KArgs qa{c->mid, c->midq, I, P, grouped ? c->mh : nullptr};
     Q8KArgs qb{c->sh_mid, c->sh_midq, Is, T};
     Q80Args q80{c->sh_mid, c->sh_q80, c->sh_s80, Is, T, grouped ? c->shh : nullptr};
     DSM_TRY(midq_impl(&qa, cf.shared_fmt == 1 ? &qb : nullptr, cf.shared_fmt == 0 ? &q80 : nullptr, stream));
@@ -1153,12 +861,9 @@ int dsmoe_forward(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t 
     StageScope sc(c, DSMOE_STAGE_DN, stream);
     DnArgs a{};
     Shape s1, s2{0, 64, 0};
-    const bool pers = !grouped && c->persistent;
-    // row-streaming launch (default, when the shapes fit) or per-item launch
-    const bool rows = !grouped && !pers && c->block_dn == 0 && dn_rows_fits(I, K) &&
-                      (cf.shared_fmt != 0 || q80_rows_fits(Is));
-    const int mb = pers ? 256 : rows ? 256 : (c->block_dn ? c->block_dn : 1024);
-    a.dn = down_args(w->down, c->midq, sel, nullptr, routed_out, d, I, K, T, &s1, mb);
+    const bool rows = !grouped && dn_rows_fits(I, K) && (cf.shared_fmt != 0 || q80_rows_fits(Is));
+    const int mb = rows ? 256 : 1024;
+    a.dn = down_args(w->down, c->midq, sel, nullptr, routed_out, d, I, K, E, T, &s1, mb);
     a.dn_tiles = s1.tiles;
     a.dn_work = grouped ? 0 : T;
     if (grouped) {
@@ -1176,7 +881,7 @@ int dsmoe_forward(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t 
                           std::min(512, mb));
       lds = std::max(lds, q80_lds(Is / 32, 1, s2.R));
     } else if (cf.shared_fmt == 1) {
-      a.sh_q2k = down_args(w->sh_down, c->sh_midq, nullptr, nullptr, shared_out, d, Is, 1, T, &s2, mb);
+      a.sh_q2k = down_args(w->sh_down, c->sh_midq, nullptr, nullptr, shared_out, d, Is, 1, 1, T, &s2, mb);
       lds = std::max(lds, down_lds(1, Is / 256, s2.R));
     }
     if (cf.shared_fmt >= 0) { a.sh_tiles = s2.tiles; a.sh_work = T; }
@@ -1185,28 +890,18 @@ int dsmoe_forward(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t 
       StageScope sg(c, DSMOE_STAGE_SH_DN, stream);
       DSM_TRY(dsmoe_q8_0_gemm(w->sh_down, nullptr, c->shh, c->sh_s80, shared_out, Is, d, T, 0.0f, stream));
     }
-    if (pers) {
-      a.sh_lds_offset = align_up((int)down_lds(K, I / 256, s1.R), 16);
-      if (cf.shared_fmt == 0) lds = a.sh_lds_offset + q80_lds(Is / 32, 1, s2.R);
-      int grid = 0;
-      DSM_TRY(persistent_grid(c, K_DN_P, lds, a.dn_tiles * a.dn_work + a.sh_tiles * a.sh_work, &grid));
-      DSM_TRY(launch(K_DN_P, dim3(grid), dim3(256), lds, stream, a));
-    } else {
-      a.interleave = (c->interleave & 8) ? 2 : ((c->interleave >> 1) & 1);
-      if (rows) {
-        a.dn_tiles = (d + kDnRowsR - 1) / kDnRowsR;
-        lds = down_lds(K, I / 256, 0);
-        if (cf.shared_fmt == 0) {
-          a.sh_tiles = q80_rows_tiles(d, false);
-          lds = std::max(lds, q80_rows_lds(Is / 32));
-        } else if (cf.shared_fmt == 1) {
-          lds = std::max(lds, down_lds(1, Is / 256, s2.R));
-        }
+    if (rows) {
+      a.dn_tiles = (d + kDnRowsR - 1) / kDnRowsR;
+      lds = down_lds(K, I / 256, 0);
+      if (cf.shared_fmt == 0) {
+        a.sh_tiles = q80_rows_tiles(d, false);
+        lds = std::max(lds, q80_rows_lds(Is / 32));
+      } else if (cf.shared_fmt == 1) {
+        lds = std::max(lds, down_lds(1, Is / 256, s2.R));
       }
-      DSM_TRY(launch(rows ? K_DN_ROWS : K_DN, dim3(a.dn_tiles * a.dn_work + a.sh_tiles * a.sh_work),
-                     dim3(rows ? 256 : std::max(s1.block, s2.block)),
-                     lds, stream, a));
     }
+    DSM_TRY(launch(rows ? K_DN_ROWS : K_DN, dim3(a.dn_tiles * a.dn_work + a.sh_tiles * a.sh_work),
+                   dim3(rows ? 256 : std::max(s1.block, s2.block)), lds, stream, a));
   }
   return DSMOE_OK;
 }

@@ -57,13 +57,13 @@ struct GateUpArgs {
   const uint8_t* gate;     // [E][I][d/256] x 66 B
   const uint8_t* up;
   const uint8_t* xq;       // Q8_K [T][d/256]
-  const int32_t* selected; // [T*k] (null: expert = slot, weight 1: shared expert)
+  const int32_t* selected; // [T*k] (null: expert 0, weight 1: shared expert); ids outside [0,E) read expert 0
   const float* weights;    // [T*k] (null: weight 1)
   const uint32_t* pair_list;
   float* gate_out;         // [pairs][I] or null
   float* up_out;           // [pairs][I] or null
   float* mid_out;          // [pairs][I]
-  int32_t d, I, k, rows_per_wg;
+  int32_t d, I, k, rows_per_wg, E;
   float clamp;
 };
 
@@ -73,10 +73,10 @@ struct GateUpArgs {
 struct DownArgs {
   const uint8_t* down;      // [E][d][I/256] x 84 B
   const uint8_t* midq;      // Q8_K [T*k][I/256]
-  const int32_t* selected;  // [T*k] (null: expert 0)
+  const int32_t* selected;  // [T*k] (null: expert 0); ids outside [0,E) read expert 0
   float* out;               // [T][d] or null
   float* down_out;          // [T*k][d] or null
-  int32_t d, I, k, rows_per_wg;
+  int32_t d, I, k, rows_per_wg, E;
 };
 
 // Q8_0 x Q8_0-activation matvec (shared expert), optionally two matrices
@@ -114,11 +114,8 @@ struct UpArgs {
   int32_t gu_tiles, gu_work; // grid = gu_tiles x gu_work
   int32_t sh_tiles, sh_work;
   int32_t sh_fmt;
-  int32_t sh_lds_offset = 0;  // dsmoe_up_p: LDS byte offset of the Q8_0 shared-expert layout
-  int32_t interleave = 0;     // dsmoe_up / dsmoe_up_rows: 1 alternates routed and shared workgroups, 2 puts the shared first
   RouterSelectArgs sel;       // dsmoe_up_rows with fuse_sel: every routed workgroup runs the selection itself
   int32_t fuse_sel = 0;       // 0, or P = E / 64 (1, 2, 4): experts per lane of the one-wave selection
-  uint64_t* trace = nullptr;  // optional (dsmoe_set_trace): 8 words per unit of dsmoe_up_p
   // dsmoe_up_rows with fuse_midq: the workgroup that completes the 256 rows
   // of a (pair, block) writes its Q8_K (midq), the one that completes a
   // token's 256-row group of the Q8_0 shared mid writes its 8 Q8_0 blocks
@@ -146,89 +143,10 @@ struct DnArgs {
   int32_t dn_tiles, dn_work;
   int32_t sh_tiles, sh_work;
   int32_t sh_fmt;
-  int32_t sh_lds_offset = 0;  // dsmoe_dn_p: LDS byte offset of the Q8_0 shared-expert layout
-  int32_t interleave = 0;     // dsmoe_dn / dsmoe_dn_rows: 1 alternates routed and shared workgroups, 2 puts the shared first
 };
 
-// Whole-layer decode in one persistent launch (dsmoe_decode).  Workgroups
-// take roles in dependency order by blockIdx.x:
-//   q8k(x) | q80(x) | router rows | shared up | routed up | shared down | routed down
-// and hand results on through agent-scope counters in `sync` (see the
-// kernel).  Every role runs on 256 threads.
-struct DecodeArgs {
-  RouterLogitsArgs router;
-  Q8KArgs q8k;
-  Q80Args q80;
-  RouterSelectArgs sel;
-  GateUpArgs gu;
-  GateUpArgs sh_iq2;
-  Q80MatvecArgs sh_q80;
-  Q8KArgs midq;       // routed mid rows -> Q8_K
-  Q8KArgs sh_midq8k;  // shared mid -> Q8_K (shared_fmt 1)
-  Q80Args sh_midq80;  // shared mid -> Q8_0 (shared_fmt 0)
-  DownArgs dn;
-  DownArgs sh_q2k;
-  Q80MatvecArgs sh_dn;
-  uint32_t* sync;     // hand-off words, see SyncMap
-  int32_t sh_fmt, T, K;
-  int32_t n_q8k, n_q80, n_router, n_shup, n_gu, n_shdn, n_dn;
-  int32_t shup_tiles, gu_tiles, shdn_tiles, dn_tiles;
-  // word offsets in `sync`
-  int32_t flags;          // readiness flags, kFlagWords each (replicated)
-  int32_t tr_q8k, tr_q80, tr_router;  // fan-in trees over the producers of each stage
-  int32_t tr_tokmid, tr_tokmid_stride;  // per token: the k * I/256 quantized mid blocks
-  int32_t tr_sh, tr_sh_stride;          // per token: the shared mid row groups
-  int32_t midrows, shrows;              // row counters per (pair, 256-row block) / (token, group)
-  uint32_t epoch;         // this launch's flag value (the host counts launches)
-  uint32_t spin_limit;
-  uint32_t poll_sleep;    // s_sleep 1 (64 clocks) steps between two polls of a flag
-  int32_t hold_streams;   // 1: the shared-expert units also wait for the routing
-  uint64_t* trace;        // optional: 8 words per unit {start, last wait done, end, role << 32 | hw id, role stamps} (100 MHz clock)
-};
-
-// Three-launch decode (T <= 8): stage A = router rows (the last one runs the
-// selection) + Q8_K(x) + shared gate/up (each workgroup quantizes x to
-// Q8_0 itself); stage B = routed gate/up (the workgroup completing a
-// 256-row block of a pair quantizes it to Q8_K) + shared down (each
-// workgroup quantizes the shared mid itself); stage C = routed down (DnArgs).
-struct StageAArgs {
-  RouterLogitsArgs router;
-  RouterSelectArgs sel;
-  Q8KArgs q8k;
-  Q80MatvecArgs sh_q80;   // xq/xscale unused: staged from `x` in the workgroup
-  const float* x;         // [T][d]
-  uint32_t* sync;         // fan-in tree over the router workgroups
-  int32_t n_router, n_q8k, n_shup, shup_tiles;
-};
-struct StageBArgs {
-  GateUpArgs gu;
-  Q80MatvecArgs sh_dn;    // xq/xscale unused: staged from `sh_mid` in the workgroup
-  Q8KArgs midq;
-  const float* sh_mid;    // [T][I_s]
-  uint32_t* sync;         // per (pair, 256-row block) row counters
-  int32_t n_gu, gu_tiles, n_shdn, shdn_tiles;
-};
-
-// Readiness flags of DecodeArgs: flag f occupies kFlagWords words at
-// sync[flags + f*kFlagWords]; its kFlagReplicas copies sit 128 bytes apart so
-// waiting workgroups poll different cache lines.  Word 0 of `sync` is the
-// sticky error word.
-enum : int32_t {
-  kFlagReplicas = 64, kFlagStride = 32, kFlagWords = kFlagReplicas * kFlagStride,
-  kFlagXq8k = 0, kFlagX80 = 1, kFlagRouted = 2, kFlagTok0 = 3,  // kFlagTok0 + t, then kFlagSh0 + t
-  kMaxDecodeT = 8, kFlagSh0 = kFlagTok0 + kMaxDecodeT, kNumFlags = kFlagSh0 + kMaxDecodeT,
-  kSyncErr = 0, kFanIn = 16
-};
-
-// Words of a fan-in tree over n producers.
-inline int32_t tree_words(int32_t n) {
-  int32_t w = 0;
-  while (n > 1) {
-    n = (n + kFanIn - 1) / kFanIn;
-    w += n;
-  }
-  return w + 1;
-}
+// Largest token count of the row-streaming (decode) launches.
+constexpr int32_t kMaxDecodeT = 8;
 
 // Grouped (sorted-by-expert) routed gate/up/SwiGLU on MFMA, for batches
 // (dsmoe_gemm.hip).  A workgroup computes one tile: up to kGuBM pairs of one

@@ -26,7 +26,8 @@ using namespace dsm;
 namespace {
 
 // Accesses to data that other workgroups of the same launch produce or
-// consume (kCoh = true, the one-launch decode path) are agent-scope relaxed
+// consume (kCoh = true: the mid rows that dsmoe_up_rows quantizes in the
+// workgroup completing a 256-row block) are agent-scope relaxed
 // atomics: they compile to plain loads/stores with the device-coherence bit,
 // which needs no L2 write-back or invalidate.  Ordering comes from waiting for
 // the stores (s_waitcnt) before a counter is bumped.  With kCoh = false they
@@ -248,7 +249,7 @@ __device__ __forceinline__ uint32_t ord_f32(float f) {
 // the f16 row (each wave-wide load is one 128-byte line) and of the first
 // token's x together, so the row's HBM latency and x's cache latency overlap.
 template <bool kCoh>
-__device__ __forceinline__ void role_router_logits(const RouterLogitsArgs& a, int bx, uint8_t* smem, uint64_t* tr = nullptr) {
+__device__ __forceinline__ void role_router_logits(const RouterLogitsArgs& a, int bx, uint8_t* smem) {
   const int row = bx % a.E, t0 = (bx / a.E) * 8, tx = threadIdx.x;
   const int nt = min(8, a.T - t0);
   const int d = a.d;  // d % 256 == 0 and d <= 8192 checked on the host
@@ -268,7 +269,6 @@ __device__ __forceinline__ void role_router_logits(const RouterLogitsArgs& a, in
   float w[32];
 #pragma unroll
   for (int j = 0; j < 32; j++) w[j] = f16_to_f32_ftz((uint16_t)wh[j]);
-  if (tr && tx == 0) tr[4] = __builtin_amdgcn_s_memrealtime();
   for (int t = 0; t < nt; t++) {
     if (t > 0) {
       const float* xr = a.x + (size_t)(t0 + t) * d + tx;
@@ -284,7 +284,6 @@ __device__ __forceinline__ void role_router_logits(const RouterLogitsArgs& a, in
     part[t][tx] = acc;
   }
   __syncthreads();
-  if (tr && tx == 0) tr[5] = __builtin_amdgcn_s_memrealtime();
   // halving tree: levels 128 and 64 cross waves (LDS), levels 32..1 inside
   // wave 0 (shuffle down: lane l adds lane l + s, the same pairs in the same order)
   for (int s2 = 128; s2 >= 64; s2 >>= 1) {
@@ -300,7 +299,6 @@ __device__ __forceinline__ void role_router_logits(const RouterLogitsArgs& a, in
       if (tx == 0) stc<kCoh>(a.out + (size_t)(t0 + t) * a.E + row, v);
     }
   }
-  if (tr && tx == 0) tr[6] = __builtin_amdgcn_s_memrealtime();
 }
 
 // ---------------------------------------------------------------------------
@@ -630,7 +628,7 @@ __device__ __forceinline__ void role_gate_up(const GateUpArgs& a, int tile, int 
   const int pair = a.pair_list ? (int)a.pair_list[work] : work;
   const int tok = pair / a.k;
   int e = a.selected ? ldc<kCoh>(a.selected + pair) : 0;
-  if (e < 0) e = 0;
+  if ((unsigned)e >= (unsigned)a.E) e = 0;  // negative ids (moe.rs:299-312) and ids past E read expert 0
   const int row0 = tile * R;
   const int items = 2 * R * (nb >> 1);
   const int B = blockDim.x;
@@ -734,7 +732,7 @@ __device__ __forceinline__ float key_score(uint64_t k) {
 // With s_sel / s_w the k results also go to LDS (slot r at index r), and
 // `global` says whether they go to a.selected / a.weights.
 template <bool kCoh, int P>
-__device__ __forceinline__ void select_wave(const RouterSelectArgs& a, int t, uint64_t* tr, int32_t* s_sel = nullptr,
+__device__ __forceinline__ void select_wave(const RouterSelectArgs& a, int t, int32_t* s_sel = nullptr,
                                             float* s_w = nullptr, bool global = true) {
   const int lane = threadIdx.x & 63;
   const int E = a.E, K = a.k, G = a.n_group > 1 ? a.n_group : 1, gsz = E / G;
@@ -754,7 +752,6 @@ __device__ __forceinline__ void select_wave(const RouterSelectArgs& a, int t, ui
     key[i] = sc > -__builtin_inff() ? (((uint64_t)ord_f32(sc) << 32) | (0xFFFFFFFFu - (uint32_t)e)) : 0ull;
     if (a.probs) a.probs[(size_t)t * E + e] = pv[i];
   }
-  if (tr && lane == 0) tr[5] = __builtin_amdgcn_s_memrealtime();
   if (G > 1) {
     // top-2 keys of this lane, then of the group's lanes
     Top2 tp{0ull, 0ull};
@@ -786,7 +783,6 @@ __device__ __forceinline__ void select_wave(const RouterSelectArgs& a, int t, ui
       for (int i = 0; i < P; i++) key[i] = 0ull;
     }
   }
-  if (tr && lane == 0) tr[6] = __builtin_amdgcn_s_memrealtime();
   // k rounds of arg-max; lane r keeps slot r
   int my_sel = -1;
   float my_p = 0.0f;
@@ -931,9 +927,9 @@ __device__ __forceinline__ void role_gate_up_rows(const GateUpArgs& a, int tile,
   if (rs) {
     if (wv == 0) {
       const bool g = tile == 0 && pair % a.k == 0;
-      if (rsP == 4) select_wave<false, 4>(*rs, tok, nullptr, g_sel_rows, g_wgt_rows, g);
-      else if (rsP == 2) select_wave<false, 2>(*rs, tok, nullptr, g_sel_rows, g_wgt_rows, g);
-      else select_wave<false, 1>(*rs, tok, nullptr, g_sel_rows, g_wgt_rows, g);
+      if (rsP == 4) select_wave<false, 4>(*rs, tok, g_sel_rows, g_wgt_rows, g);
+      else if (rsP == 2) select_wave<false, 2>(*rs, tok, g_sel_rows, g_wgt_rows, g);
+      else select_wave<false, 1>(*rs, tok, g_sel_rows, g_wgt_rows, g);
     }
     __syncthreads();
     e = g_sel_rows[pair % a.k];
@@ -942,7 +938,7 @@ __device__ __forceinline__ void role_gate_up_rows(const GateUpArgs& a, int tile,
     e = a.selected ? a.selected[pair] : 0;
     wgt = a.weights ? a.weights[pair] : 1.0f;
   }
-  if (e < 0) e = 0;
+  if ((unsigned)e >= (unsigned)a.E) e = 0;  // negative ids (moe.rs:299-312) and ids past E read expert 0
   const int row0 = tile * 32, mat = wv >> 1, rr = (wv & 1) * 16 + (lane >> 2), j = lane & 3;
   const int row = min(row0 + rr, a.I - 1);
   const size_t row_bytes = (size_t)nb * IQ2XXS_BYTES;
@@ -1025,7 +1021,7 @@ __device__ __forceinline__ void role_down(const DownArgs& a, int tile, int tok, 
     have = row0 + rr < a.d;
     if (!have) return;
     int e = a.selected ? ldc<kCoh>(a.selected + tok * K + s) : 0;
-    if (e < 0) e = 0;
+    if ((unsigned)e >= (unsigned)a.E) e = 0;  // negative ids (moe.rs:299-312) and ids past E read expert 0
     const uint8_t* src = a.down + (size_t)e * exp_bytes + (size_t)(row0 + rr) * row_bytes + (size_t)b * Q2K_BYTES;
 #pragma unroll
     for (int q = 0; q < 5; q++) {
@@ -1085,7 +1081,7 @@ __device__ __forceinline__ void role_down_rows(const DownArgs& a, int tile, int 
   uint8_t* s_q8 = (uint8_t*)(s_bs + K * nb * 16);
   const int slot = lane >> 3, j = lane & 7, sl = min(slot, K - 1);
   int e = a.selected ? a.selected[tok * K + sl] : 0;
-  if (e < 0) e = 0;
+  if ((unsigned)e >= (unsigned)a.E) e = 0;  // negative ids (moe.rs:299-312) and ids past E read expert 0
   const size_t row_bytes = (size_t)nb * Q2K_BYTES;
   const int row0 = tile * 4 * kRpw;
   // the activation words are loaded first (cache hits) so that the LDS
@@ -1521,75 +1517,9 @@ __device__ __forceinline__ void dn_unit(const DownArgs& a, int tile, int tok, ui
     }
 }
 
-// Units u, u + stride, ... < end, each loaded (load(u, regs)) one unit ahead
-// of its computation (run(u, regs)); two register sets alternate.
-template <int N>
-struct UnitRegs {
-  uint32_t w[N];
-};
-template <int N, class Load, class Run>
-__device__ __forceinline__ void pipelined_units(int u, int end, int stride, Load load, Run run) {
-  if (u >= end) return;
-  UnitRegs<N> ra, rb;
-  load(u, ra.w);
-  while (true) {
-    int un = u + stride;
-    if (un < end) load(un, rb.w);
-    run(u, (const uint32_t*)ra.w);
-    if (un >= end) break;
-    u = un;
-    un = u + stride;
-    if (un < end) load(un, ra.w);
-    run(u, (const uint32_t*)rb.w);
-    if (un >= end) break;
-    u = un;
-  }
-}
-
-// A workgroup's schedule over two unit lists: units b, b + G, ... of list A
-// (n_a of them) and of list B (n_b), alternating A, B, A, ... (B first for
-// odd b), then the rest of whichever list is longer.  Returns -1 at the end;
-// otherwise unit u of list A as u, of list B as n_a + u.
-struct TwoListSchedule {
-  int ia, ib, n_a, n_b, G;
-  bool turn_b;
-  __device__ TwoListSchedule(int b, int n_a_, int n_b_, int G_)
-      : ia(b), ib(b), n_a(n_a_), n_b(n_b_), G(G_), turn_b((b & 1) != 0) {}
-  __device__ __forceinline__ int next() {
-    const bool has_a = ia < n_a, has_b = ib < n_b;
-    if (!has_a && !has_b) return -1;
-    const bool take_b = has_b && (turn_b || !has_a);
-    turn_b = !take_b;
-    if (take_b) { const int u = ib; ib += G; return n_a + u; }
-    const int u = ia;
-    ia += G;
-    return u;
-  }
-};
-
-// As pipelined_units, over a TwoListSchedule.
-template <int N, class Load, class Run>
-__device__ __forceinline__ void pipelined_schedule(TwoListSchedule sch, Load load, Run run) {
-  int u = sch.next();
-  if (u < 0) return;
-  UnitRegs<N> ra, rb;
-  load(u, ra.w);
-  while (true) {
-    int un = sch.next();
-    if (un >= 0) load(un, rb.w);
-    run(u, (const uint32_t*)ra.w);
-    if (un < 0) break;
-    u = un;
-    un = sch.next();
-    if (un >= 0) load(un, ra.w);
-    run(u, (const uint32_t*)rb.w);
-    if (un < 0) break;
-    u = un;
-  }
-}
 
 template <bool kCoh>
-__device__ __forceinline__ void role_select(const RouterSelectArgs& a, int t, uint8_t* smem, uint64_t* tr = nullptr) {
+__device__ __forceinline__ void role_select(const RouterSelectArgs& a, int t, uint8_t* smem) {
   const int E = a.E;
   uint64_t* s_key = (uint64_t*)smem;
   uint64_t* s_gkey = s_key + E;
@@ -1608,11 +1538,10 @@ __device__ __forceinline__ void role_select(const RouterSelectArgs& a, int t, ui
     else if (select_wave_fits<kCoh, 4>(a)) fast = 4;
     if (fast) {
       if (tid < 64) {
-        if (!kCoh && fast == 1) select_wave<kCoh, 1>(a, t, tr);
-        else if (!kCoh && fast == 2) select_wave<kCoh, 2>(a, t, tr);
-        else select_wave<kCoh, 4>(a, t, tr);
+        if (!kCoh && fast == 1) select_wave<kCoh, 1>(a, t);
+        else if (!kCoh && fast == 2) select_wave<kCoh, 2>(a, t);
+        else select_wave<kCoh, 4>(a, t);
       }
-      if (tr && tid == 0) tr[7] = __builtin_amdgcn_s_memrealtime();
       __syncthreads();
       return;
     }
@@ -1629,7 +1558,6 @@ __device__ __forceinline__ void role_select(const RouterSelectArgs& a, int t, ui
   if (tid < 64) { s_b1[tid] = -__builtin_inff(); s_b2[tid] = -__builtin_inff(); s_keep[tid] = G == 1; }
   if (tid < 32) s_sel[tid] = -1;
   __syncthreads();
-  if (tr && tid == 0) tr[5] = __builtin_amdgcn_s_memrealtime();
   if (G > 1) {
     for (int e = tid; e < E; e += 256) {
       const uint64_t k0 = s_key[e];
@@ -1666,7 +1594,6 @@ __device__ __forceinline__ void role_select(const RouterSelectArgs& a, int t, ui
     if (r < K) s_sel[r] = e;
   }
   __syncthreads();
-  if (tr && tid == 0) tr[6] = __builtin_amdgcn_s_memrealtime();
   if (tid == 0) {
     float sum = 0.0f;
     for (int j = 0; j < K; j++) sum += s_sel[j] >= 0 ? s_p[s_sel[j]] : 0.0f;
@@ -1676,7 +1603,6 @@ __device__ __forceinline__ void role_select(const RouterSelectArgs& a, int t, ui
       stc<kCoh>(a.selected + (size_t)t * K + j, e);
       stc<kCoh>(a.weights + (size_t)t * K + j, (e >= 0 ? s_p[e] : 0.0f) / (sum / a.route_scale));
     }
-    if (tr) tr[7] = __builtin_amdgcn_s_memrealtime();
   }
   __syncthreads();
 }
@@ -1708,27 +1634,11 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_prep(const PrepArgs a) {
 }
 
 // Routed + shared gate/up/SwiGLU.
-// Workgroup index -> unit: the two unit lists interleave (even indices
-// take list A, odd list B, while both last), so the dispatcher alternates
-// arithmetic-heavy and bandwidth-heavy workgroups on every compute unit.
-// Returns the index in [A units][B units].
-__device__ __forceinline__ int interleave2(int w, int n_a, int n_b) {
-  const int lo = min(n_a, n_b);
-  if (w < 2 * lo) return (w & 1) ? n_a + (w >> 1) : (w >> 1);
-  return n_a > n_b ? w - lo : n_a + (w - lo);
-}
-// Dispatch order of a two-list launch: 0 = list A first, 1 = alternating,
-// 2 = list B first.
-__device__ __forceinline__ int order2(int w, int n_a, int n_b, int mode) {
-  if (mode == 1) return interleave2(w, n_a, n_b);
-  if (mode == 2) return w < n_b ? n_a + w : w - n_b;
-  return w;
-}
-
+// Workgroups [routed units][shared units].
 extern "C" __global__ __launch_bounds__(1024) void dsmoe_up(const UpArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int n_gu = a.gu_tiles * a.gu_work;
-  int w = order2(blockIdx.x, n_gu, a.sh_tiles * a.sh_work, a.interleave);
+  int w = blockIdx.x;
   if (w < n_gu) { role_gate_up<false>(a.gu, w % a.gu_tiles, w / a.gu_tiles, smem); return; }
   w -= n_gu;
   if (w < a.sh_tiles * a.sh_work) {
@@ -1738,7 +1648,7 @@ extern "C" __global__ __launch_bounds__(1024) void dsmoe_up(const UpArgs a) {
 }
 
 // Routed gate/up in the row-streaming form (32 rows of one pair per
-// workgroup) + the shared expert's workgroups, in the order a.interleave picks.
+// workgroup) + the shared expert's workgroups.
 __device__ __forceinline__ void role_gate_up_rows_any(const UpArgs& a, int tile, int pair, uint8_t* smem) {
   const RouterSelectArgs* rs = a.fuse_sel ? &a.sel : nullptr;
   switch ((a.gu.d + 1023) >> 10) {  // blocks per lane (d <= 8192)
@@ -1774,7 +1684,7 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_up_rows(const UpArgs a) 
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ int s_flag;
   const int n_gu = a.gu_tiles * a.gu_work;
-  int w = order2(blockIdx.x, n_gu, a.sh_tiles * a.sh_work, a.interleave);
+  int w = blockIdx.x;
   auto arrive = [&](uint32_t* c, uint32_t n, uint32_t target) {
     return stores_done_then(&s_flag, [&] {
       if (__hip_atomic_fetch_add(c, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + n != target) return false;
@@ -1817,121 +1727,6 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_up_rows(const UpArgs a) 
   }
 }
 
-// Decode (T <= 8) gate/up as a persistent grid (G = gridDim.x workgroups,
-// sized to what the GPU holds at once).  The shared-expert units (Q8_0:
-// bandwidth-heavy, little arithmetic) and the routed units (IQ2_XXS: heavy
-// arithmetic) are interleaved so that every workgroup alternates between
-// them and the compute units stream one kind while computing the other.
-// Each unit is loaded one unit ahead of its computation; the IQ2_XXS tables
-// and the staged activations stay in LDS from unit to unit (kept apart:
-// the Q8_0 staging sits above the gate/up layout).  One work item per
-// thread per unit (rows_per_wg chosen for 256 threads).
-extern "C" __global__ __launch_bounds__(256) void dsmoe_up_p(const UpArgs a) {
-  extern __shared__ __align__(16) uint8_t smem[];
-  const int G = gridDim.x, tid = threadIdx.x;
-  const int n_sh = a.sh_fmt == 0 ? a.sh_tiles * a.sh_work : 0, n_gu = a.gu_tiles * a.gu_work;
-  if (a.sh_fmt == 1) {  // IQ2_XXS shared expert: plain loop ahead of the routed units
-    for (int u = blockIdx.x; u < a.sh_tiles * a.sh_work; u += G) {
-      role_gate_up<false>(a.sh_iq2, u % a.sh_tiles, u / a.sh_tiles, smem);
-      __syncthreads();
-    }
-  }
-  const GateUpArgs& g = a.gu;
-  const Q80MatvecArgs& q = a.sh_q80;
-  const int Rg = g.rows_per_wg, Rs = q.rows_per_wg, nb = g.d >> 8;
-  uint8_t* smem_q80 = smem + a.sh_lds_offset;
-  int tag_gu = -1, tag_sh = -1;
-  auto kind_of = [&](int u) { return u < n_gu ? 1 : 0; };  // u: [routed units][shared units]
-  pipelined_schedule<33>(
-      TwoListSchedule(blockIdx.x, n_gu, n_sh, G),
-      [&](int u, uint32_t* wv) {
-        if (kind_of(u)) {
-          const int row0 = (u % a.gu_tiles) * Rg, pair = u / a.gu_tiles;
-          int e = g.selected ? g.selected[pair] : 0;
-          if (e < 0) e = 0;
-          gu_load(g, e, row0, gu_item(g, row0, tid), wv);
-        } else {
-          const int us = u - n_gu, row0 = (us % a.sh_tiles) * Rs;
-          q80_load<32>(q, row0, q80_item(q, row0, tid), wv);
-        }
-      },
-      [&](int u, const uint32_t* wv) {
-        uint64_t* tr = a.trace ? a.trace + 8 * u : nullptr;
-        if (tr && tid == 0) tr[0] = __builtin_amdgcn_s_memrealtime();
-        if (kind_of(u)) {
-          const int row0 = (u % a.gu_tiles) * Rg, pair = u / a.gu_tiles, tok = pair / g.k;
-          const GuLds l = gu_lds(g, smem);
-          if (tag_gu != tok) {
-            load_iq2_tables(l.tab);
-            stage_q8k<false>(g.xq + (size_t)tok * nb * Q8K_BYTES, nb, l.q8, l.yd, nullptr);
-            tag_gu = tok;
-          }
-          __syncthreads();
-          if (tr && tid == 0) tr[4] = __builtin_amdgcn_s_memrealtime();
-          gu_compute(g, gu_item(g, row0, tid), wv, l);
-          __syncthreads();
-          if (tr && tid == 0) tr[5] = __builtin_amdgcn_s_memrealtime();
-          gu_epilogue<false>(g, pair, row0, g.weights ? g.weights[pair] : 1.0f, l);
-        } else {
-          const int us = u - n_gu, tile = us % a.sh_tiles, tok = us / a.sh_tiles;
-          q80_unit<false, 32>(q, tile, tok, smem_q80, wv, tag_sh != tok);
-          tag_sh = tok;
-        }
-        if (tr && tid == 0) {
-          tr[2] = __builtin_amdgcn_s_memrealtime();
-          tr[3] = ((uint64_t)(kind_of(u) ? 4 : 3) << 32) | __smid();
-          tr[6] = blockIdx.x;
-        }
-      });
-}
-
-// Decode (T <= 8) down as a persistent grid: routed units (all k slots of a
-// token, summed in slot order) interleaved with shared-expert units, each
-// loaded one unit ahead; the staged activations stay in LDS (the Q8_0
-// staging sits above the routed layout).
-extern "C" __global__ __launch_bounds__(256) void dsmoe_dn_p(const DnArgs a) {
-  extern __shared__ __align__(16) uint8_t smem[];
-  const int G = gridDim.x, tid = threadIdx.x;
-  const DownArgs& dn = a.dn;
-  const Q80MatvecArgs& q = a.sh_q80;
-  const int R = dn.rows_per_wg, K = dn.k, Rs = q.rows_per_wg;
-  const int n_dn = a.dn_tiles * a.dn_work, n_sh = a.sh_fmt == 0 ? a.sh_tiles * a.sh_work : 0;
-  uint8_t* smem_q80 = smem + a.sh_lds_offset;
-  int tag_dn = -1, tag_sh = -1;
-  pipelined_schedule<21>(
-      TwoListSchedule(blockIdx.x, n_dn, n_sh, G),
-      [&](int u, uint32_t* wv) {
-        if (u < n_dn) {
-          const int row0 = (u % a.dn_tiles) * R, tok = u / a.dn_tiles;
-          const DnItem it = dn_item(dn, row0, tid);
-          int e = (it.have && dn.selected) ? dn.selected[tok * K + it.s] : 0;
-          if (e < 0) e = 0;
-          dn_load(dn, e, row0, it, wv);
-        } else {
-          const int us = u - n_dn, row0 = (us % a.sh_tiles) * Rs;
-          q80_load<20>(q, row0, q80_item(q, row0, tid), wv);
-        }
-      },
-      [&](int u, const uint32_t* wv) {
-        if (u < n_dn) {
-          const int tile = u % a.dn_tiles, tok = u / a.dn_tiles;
-          dn_unit<false>(dn, tile, tok, smem, wv, tag_dn != tok);
-          tag_dn = tok;
-        } else {
-          const int us = u - n_dn, tile = us % a.sh_tiles, tok = us / a.sh_tiles;
-          q80_unit<false, 20>(q, tile, tok, smem_q80, wv, tag_sh != tok);
-          tag_sh = tok;
-        }
-      });
-  if (a.sh_fmt == 1) {
-    __syncthreads();
-    for (int u = blockIdx.x; u < a.sh_tiles * a.sh_work; u += G) {
-      role_down<false>(a.sh_q2k, u % a.sh_tiles, u / a.sh_tiles, smem);
-      __syncthreads();
-    }
-  }
-}
-
 // Q8_K of mid rows + Q8_0 of the shared mid (blockDim 256): four Q8_K blocks
 // per workgroup, 32 Q8_0 blocks (8 when in_dim is not a multiple of 32).
 extern "C" __global__ __launch_bounds__(256) void dsmoe_midq(const MidqArgs a) {
@@ -1959,7 +1754,7 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_midq(const MidqArgs a) {
 extern "C" __global__ __launch_bounds__(1024) void dsmoe_dn(const DnArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int n_dn = a.dn_tiles * a.dn_work;
-  int w = order2(blockIdx.x, n_dn, a.sh_tiles * a.sh_work, a.interleave);
+  int w = blockIdx.x;
   if (w < n_dn) { role_down<false>(a.dn, w % a.dn_tiles, w / a.dn_tiles, smem); return; }
   w -= n_dn;
   if (w < a.sh_tiles * a.sh_work) {
@@ -1972,7 +1767,7 @@ extern "C" __global__ __launch_bounds__(1024) void dsmoe_dn(const DnArgs a) {
 extern "C" __global__ __launch_bounds__(256) void dsmoe_dn_rows(const DnArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int n_dn = a.dn_tiles * a.dn_work;
-  int w = order2(blockIdx.x, n_dn, a.sh_tiles * a.sh_work, a.interleave);
+  int w = blockIdx.x;
   if (w < n_dn) { role_down_rows_any(a.dn, w % a.dn_tiles, w / a.dn_tiles, smem); return; }
   w -= n_dn;
   if (w < a.sh_tiles * a.sh_work) {
@@ -1984,485 +1779,6 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_dn_rows(const DnArgs a) 
 extern "C" __global__ __launch_bounds__(256) void dsmoe_router_select(const RouterSelectArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   role_select<false>(a, blockIdx.x, smem);
-}
-
-// ---------------------------------------------------------------------------
-// dsmoe_decode: the whole layer for T <= 8 tokens in one launch.
-//
-// Kernel boundaries cost several microseconds each on this GPU, more than a
-// small role's work, so the layer runs as one persistent grid.  The work is
-// a list of units in dependency order (DecodeArgs: q8k | q80 | router |
-// shared/routed up | shared down | routed down); workgroup b takes units
-// b, b + G, b + 2G, ... (G = gridDim.x, sized by the host to the number of
-// workgroups the GPU holds at once).  A unit only waits on units with a
-// smaller index, so the smallest unfinished unit is never blocked and every
-// wait ends, provided all G workgroups are resident together.  Between units
-// a workgroup keeps the IQ2_XXS tables and the staged activation in LDS.
-//
-// Hand-off protocol.  Data that crosses workgroups is written and read with
-// device-coherent accesses (ldc/stc, kCoh = true), which need no L2
-// write-back or invalidate (those are whole-cache operations that serialise
-// per XCD).  A producer waits for its stores (s_waitcnt), then arrives at a
-// counter; the arrival that completes a counter resets it to zero (so every
-// launch starts from zero without a memset) and, at the top of a fan-in-16
-// tree, publishes a readiness flag with this launch's epoch.  Flags are
-// replicated on 16 cache lines and each waiting workgroup polls its own
-// copy, so neither the arrivals nor the polls pile onto one address.
-// A wait that exceeds spin_limit sets the sticky error word instead of
-// hanging; the host reads (and clears) it with dsmoe_check.
-//
-// Stages and hand-offs:
-//   Q8_K(x), Q8_0(x)  -> flags Xq8k, X80
-//   router rows       -> the last row runs the selection (moe.rs:177-287),
-//                        then flag Routed
-//   routed up         -> per (pair, 256-row block): the workgroup completing
-//                        the block writes its Q8_K (quantize.rs:309-417);
-//                        the token's last block raises flag Tok[t]
-//   shared up         -> per 256-row group likewise, flag Sh[t]
-//   down              -> weights are loaded before the flag wait, so down
-//                        streaming overlaps the tail of the up stage
-// ---------------------------------------------------------------------------
-namespace {
-
-__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
-  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t add_agent(uint32_t* p, uint32_t v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ uint32_t* flag_word(const DecodeArgs& a, int f, int replica) {
-  return a.sync + a.flags + f * kFlagWords + (replica % kFlagReplicas) * kFlagStride;
-}
-
-// All threads: raise flag f to this launch's epoch, one replica per lane.
-__device__ __forceinline__ void publish(const DecodeArgs& a, int f) {
-  if (threadIdx.x < kFlagReplicas) st_agent(flag_word(a, f, threadIdx.x), a.epoch);
-}
-
-// All threads: wait until flag f reaches this launch's epoch.  False if the
-// wait was abandoned (error word set).
-__device__ __forceinline__ bool wait_flag(const DecodeArgs& a, int f, int* s_ok, int unit) {
-  if (threadIdx.x == 0) {
-    const uint32_t* fw = flag_word(a, f, blockIdx.x);
-    int ok = 1;
-    uint32_t n = 0;
-    while ((int32_t)(ld_agent(fw) - a.epoch) < 0) {
-      if (ld_agent(a.sync + kSyncErr) != 0u || ++n > a.spin_limit) {
-        st_agent(a.sync + kSyncErr, 1u);
-        ok = 0;
-        break;
-      }
-      for (uint32_t k = 0; k < a.poll_sleep; k++) __builtin_amdgcn_s_sleep(1);
-    }
-    *s_ok = ok;
-    if (a.trace) a.trace[8 * unit + 1] = __builtin_amdgcn_s_memrealtime();
-  }
-  __syncthreads();
-  return *s_ok != 0;
-}
-
-// Thread 0: producer `id` of `n` arrives at the fan-in tree at sync[base].
-// Returns true for the arrival that completes the whole tree.  Every node is
-// reset by the arrival that completes it.
-__device__ __forceinline__ bool tree_arrive(const DecodeArgs& a, int base, int n, int id) {
-  while (true) {
-    const int node = id / kFanIn;
-    const int target = min(kFanIn, n - node * kFanIn);
-    uint32_t* c = a.sync + base + node;
-    if (add_agent(c, 1u) + 1u != (uint32_t)target) return false;
-    st_agent(c, 0u);
-    if (n <= kFanIn) return true;
-    base += (n + kFanIn - 1) / kFanIn;
-    n = (n + kFanIn - 1) / kFanIn;
-    id = node;
-  }
-}
-
-// All threads: make this workgroup's coherent stores complete, then run
-// `f` on thread 0 and broadcast its bool result.
-template <class F>
-__device__ __forceinline__ bool after_stores(int* s_flag, F f) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) *s_flag = f() ? 1 : 0;
-  __syncthreads();
-  return *s_flag != 0;
-}
-
-// Thread 0: rows [row0, row0+R) of a 256-row block were written; true for the
-// workgroup that completes the block (it resets the counter).
-__device__ __forceinline__ bool rows_arrive(const DecodeArgs& a, int word, int rows_total, int row0, int R) {
-  const int n = min(R, rows_total - row0);
-  const int target = min(256, rows_total - ((row0 >> 8) << 8));
-  uint32_t* c = a.sync + word;
-  if (add_agent(c, (uint32_t)n) + (uint32_t)n != (uint32_t)target) return false;
-  st_agent(c, 0u);
-  return true;
-}
-
-}  // namespace
-
-// ---------------------------------------------------------------------------
-// Three-launch decode
-// ---------------------------------------------------------------------------
-namespace {
-
-// Q8_0 quantization of one activation row (quantize.rs:147-225) straight
-// into the LDS layout role_q80_matvec reads (scales, then codes): two
-// 32-element blocks per wavefront per step, amax by a 32-lane maximum (the
-// maximum of |v| does not depend on the order), codes as role_q80 rounds
-// them.  in_dim a multiple of 32.  All threads.
-__device__ __forceinline__ void q80_local(const float* x, int in_dim, uint8_t* smem) {
-  const int nb = in_dim >> 5, lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  float* s_xs = (float*)smem;
-  int8_t* s_xq = (int8_t*)(s_xs + align_up(nb, 4));
-  // step j: wavefront w quantizes blocks 2(w + nw j) and 2(w + nw j) + 1;
-  // the loads of 8 steps go out together
-  constexpr int kChunk = 8;
-  for (int j0 = 0; 2 * (wv + nw * j0) < nb; j0 += kChunk) {
-    float xv[kChunk];
-#pragma unroll
-    for (int j = 0; j < kChunk; j++) {
-      const int b = 2 * (wv + nw * (j0 + j)) + (lane >> 5);
-      xv[j] = b < nb ? x[b * 32 + (lane & 31)] : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < kChunk; j++) {
-      const int b = 2 * (wv + nw * (j0 + j)) + (lane >> 5), l = lane & 31;
-      const bool live = b < nb;
-      const float v = xv[j];
-      float am = v < 0.0f ? -v : v;
-#pragma unroll
-      for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
-      const float d = am / 127.0f;
-      const float id = d != 0.0f ? 1.0f / d : 0.0f;
-      const float raw = v * id;
-      const int8_t q = sat_i8_trunc(raw >= 0.0f ? raw + 0.5f : raw - 0.5f);
-      if (live) {
-        s_xq[b * 32 + l] = q;
-        if (l == 0) s_xs[b] = d;
-      }
-    }
-  }
-}
-
-// Thread 0: producer `id` of `n` arrives at the fan-in tree at `c`; true for
-// the arrival completing the tree (nodes reset by their completer).
-__device__ __forceinline__ bool tree_arrive_at(uint32_t* c, int n, int id) {
-  while (true) {
-    const int node = id / kFanIn;
-    const int target = min(kFanIn, n - node * kFanIn);
-    uint32_t* w = c + node;
-    if (__hip_atomic_fetch_add(w, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u != (uint32_t)target) return false;
-    __hip_atomic_store(w, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (n <= kFanIn) return true;
-    c += (n + kFanIn - 1) / kFanIn;
-    n = (n + kFanIn - 1) / kFanIn;
-    id = node;
-  }
-}
-
-template <class F>
-__device__ __forceinline__ bool stores_then(int* s_flag, F f) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) *s_flag = f() ? 1 : 0;
-  __syncthreads();
-  return *s_flag != 0;
-}
-
-}  // namespace
-
-// Stage A: [router rows][Q8_K(x)][shared gate/up].  The router rows store
-// their logits device-coherently and arrive at a fan-in tree; the last
-// arrival runs the selection (moe.rs:177-287) for every token.
-extern "C" __global__ __launch_bounds__(256) void dsmoe_stage_a(const StageAArgs a) {
-  extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ int s_flag;
-  int w = blockIdx.x;
-  if (w < a.n_router) {
-    role_router_logits<true>(a.router, w, smem);
-    if (stores_then(&s_flag, [&] { return tree_arrive_at(a.sync, a.n_router, w); }))
-      for (int t = 0; t < a.router.T; t++) role_select<true>(a.sel, t, smem);
-    return;
-  }
-  w -= a.n_router;
-  if (w < a.n_q8k) { role_q8k<false, false>(a.q8k, w, smem); return; }
-  w -= a.n_q8k;
-  if (w < a.n_shup) {
-    const int tile = w % a.shup_tiles, tok = w / a.shup_tiles;
-    role_q80_matvec<false>(a.sh_q80, tile, tok, smem, [&] {
-      q80_local(a.x + (size_t)tok * a.sh_q80.in_dim, a.sh_q80.in_dim, smem);
-      return true;
-    }, false);
-  }
-}
-
-// Stage B: [routed gate/up][shared down], 256 threads.  Routed mid rows are
-// stored device-coherently; the workgroup that completes the 256 rows of a
-// (pair, block) quantizes them to Q8_K (quantize.rs:309-417).
-extern "C" __global__ __launch_bounds__(256) void dsmoe_stage_b(const StageBArgs a) {
-  extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ int s_flag;
-  int w = blockIdx.x;
-  if (w < a.n_gu) {
-    const int tile = w % a.gu_tiles, pair = w / a.gu_tiles;
-    const int I = a.gu.I, R = a.gu.rows_per_wg, nbI = I / 256, row0 = tile * R, blk = row0 >> 8;
-    role_gate_up<true>(a.gu, tile, pair, smem);
-    if (stores_then(&s_flag, [&] {
-          const int n = min(R, I - row0), target = min(256, I - (blk << 8));
-          uint32_t* c = a.sync + pair * nbI + blk;
-          if (__hip_atomic_fetch_add(c, (uint32_t)n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + (uint32_t)n !=
-              (uint32_t)target)
-            return false;
-          __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          return true;
-        }))
-      role_q8k<true, false>(a.midq, pair * nbI + blk, smem);
-    return;
-  }
-  w -= a.n_gu;
-  if (w < a.n_shdn) {
-    const int tile = w % a.shdn_tiles, tok = w / a.shdn_tiles;
-    role_q80_matvec<false>(a.sh_dn, tile, tok, smem, [&] {
-      q80_local(a.sh_mid + (size_t)tok * a.sh_dn.in_dim, a.sh_dn.in_dim, smem);
-      return true;
-    }, false);
-  }
-}
-
-// The decode kernel's argument block, re-read from the kernel-argument
-// segment: the opaque pointer keeps the compiler from hoisting every phase's
-// arguments out of the persistent loops (they would not fit the scalar
-// registers and would spill into vector registers).  Loads stay scalar.
-typedef const __attribute__((address_space(4))) DecodeArgs* DecodeArgsPtr;
-__device__ __forceinline__ DecodeArgsPtr decode_args() {
-  DecodeArgsPtr p = (DecodeArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
-  asm volatile("" : "+s"(p));
-  return p;
-}
-
-extern "C" __global__ __launch_bounds__(256) void dsmoe_decode(const DecodeArgs a) {
-  extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ int s_ok, s_flag;
-  const int K = a.K;
-  const int G = gridDim.x;
-  // What the LDS holds between units: tag = kind * 16 + token of the staged
-  // activation (kind 1 = IQ2 tables + Q8_K(x), 2 = Q8_0(x), 3 = Q8_K(mid) of
-  // the routed slots, 4 = Q8_0(shared mid), 5 = Q8_K(shared mid)); -1 after a
-  // role that reuses the whole LDS.  Uniform across the workgroup.
-  int tag = -1;
-  uint32_t seen = 0;  // flags already observed at this epoch (uniform)
-  int cur = 0;        // current unit (trace)
-  auto wait_once = [&](const DecodeArgs& A, int f) {
-    const uint32_t bit = 1u << f;
-    if (seen & bit) return true;
-    const bool ok = wait_flag(A, f, &s_ok, cur);
-    if (ok) seen |= bit;
-    return ok;
-  };
-  auto begin = [&](const DecodeArgs& A, int u) {
-    cur = u;
-    if (A.trace && threadIdx.x == 0) {
-      A.trace[8 * u] = __builtin_amdgcn_s_memrealtime();
-      A.trace[8 * u + 1] = 0;
-    }
-  };
-  // role: q8k, q80, router, shared up, routed up, shared down, down
-  auto end = [&](const DecodeArgs& A, int u, int role) {
-    if (A.trace && threadIdx.x == 0) {
-      A.trace[8 * u + 2] = __builtin_amdgcn_s_memrealtime();
-      A.trace[8 * u + 3] = ((uint64_t)role << 32) | __smid();
-    }
-    __syncthreads();  // the role's last LDS reads finish before the next unit stages
-  };
-  // Phases in unit order; each loop visits this workgroup's units of its
-  // phase (u = blockIdx.x mod G).  One loop per phase keeps only that phase's
-  // arguments live.
-  int base = 0;
-  auto first = [&](int n) { return base + (int)((blockIdx.x - base % G + G) % G); };
-
-  // Q8_K(x), Q8_0(x)
-  for (int u = first(a.n_q8k); u < base + a.n_q8k; u += G) {
-    const DecodeArgs A = *decode_args();
-    begin(A, u);
-    const int w = u - base;
-    role_q8k<false, true>(A.q8k, w, smem);
-    if (after_stores(&s_flag, [&] { return tree_arrive(A, A.tr_q8k, A.n_q8k, w); })) publish(A, kFlagXq8k);
-    end(A, u, 0);
-  }
-  base += a.n_q8k;
-  for (int u = first(a.n_q80); u < base + a.n_q80; u += G) {
-    const DecodeArgs A = *decode_args();
-    begin(A, u);
-    const int w = u - base;
-    role_q80<false, true>(A.q80, w, smem);
-    if (after_stores(&s_flag, [&] { return tree_arrive(A, A.tr_q80, A.n_q80, w); })) publish(A, kFlagX80);
-    end(A, u, 1);
-  }
-  base += a.n_q80;
-  // router rows; the last one runs the selection
-  for (int u = first(a.n_router); u < base + a.n_router; u += G) {
-    const DecodeArgs A = *decode_args();
-    begin(A, u);
-    const int w = u - base;
-    // the router and the selection are the critical path of the launch:
-    // their waves win issue arbitration against co-resident streaming waves
-    __builtin_amdgcn_s_setprio(2);
-    role_router_logits<true>(A.router, w, smem, A.trace ? A.trace + 8 * u : nullptr);
-    if (after_stores(&s_flag, [&] { return tree_arrive(A, A.tr_router, A.n_router, w); })) {
-      if (A.trace && threadIdx.x == 0) A.trace[8 * u + 4] = __builtin_amdgcn_s_memrealtime();
-      for (int t = 0; t < A.T; t++) role_select<true>(A.sel, t, smem, A.trace ? A.trace + 8 * u : nullptr);
-      // "routed" also promises Q8_K(x): consumers then wait on one flag
-      if (wait_once(A, kFlagXq8k) && after_stores(&s_flag, [] { return true; })) publish(A, kFlagRouted);
-    }
-    __builtin_amdgcn_s_setprio(0);
-    end(A, u, 2);
-  }
-  base += a.n_router;
-  tag = -1;
-  // shared-up tiles first: they need only Q8(x) and stream while the
-  // router and the selection run
-  for (int u = first(a.n_shup); u < base + a.n_shup; u += G) {
-    const DecodeArgs A = *decode_args();
-    begin(A, u);
-    const int idx = u - base;
-    const int tile = idx % A.shup_tiles, tok = idx / A.shup_tiles;
-    const int Is = A.sh_fmt == 0 ? A.sh_q80.out_dim : A.sh_iq2.I;
-    const int R = A.sh_fmt == 0 ? A.sh_q80.rows_per_wg : A.sh_iq2.rows_per_wg;
-    const int ngroups = (Is + 255) / 256, g = (tile * R) >> 8;
-    bool ok = true;
-    // streaming starts only once the routing is done: the router rows and
-    // the selection are the critical path, and memory traffic of other
-    // workgroups on the same compute units delays their every access
-    if (A.hold_streams) ok = wait_once(A, kFlagRouted);
-    if (!ok) {
-    } else if (A.sh_fmt == 0) {
-      const int want = 2 * 16 + tok;
-      role_q80_matvec<true>(A.sh_q80, tile, tok, smem, [&] { return ok = wait_once(A, kFlagX80); }, tag != want);
-      tag = want;
-    } else {
-      const int want = 1 * 16 + tok;
-      role_gate_up<true>(A.sh_iq2, tile, tok, smem, [&] { return ok = wait_once(A, kFlagXq8k); }, tag != want);
-      tag = want;
-    }
-    if (ok && after_stores(&s_flag, [&] { return rows_arrive(A, A.shrows + tok * ngroups + g, Is, tile * R, R); })) {
-      if (A.sh_fmt == 0)  // Q8_0 blocks 8g .. 8g+7 of this token's shared mid (one role_q80 unit)
-        role_q80<true, true>(A.sh_midq80, tok * ((Is / 32 + 7) / 8) + g, smem);
-      else
-        role_q8k<true, true>(A.sh_midq8k, tok * (Is / 256) + g, smem);
-      tag = -1;
-      if (after_stores(&s_flag, [&] { return tree_arrive(A, A.tr_sh + tok * A.tr_sh_stride, ngroups, g); }))
-        publish(A, kFlagSh0 + tok);
-    }
-    end(A, u, 3);
-  }
-  base += a.n_shup;
-  // routed-up tiles, software-pipelined: the next tile's weights are loaded
-  // before the current tile is computed, so their HBM latency overlaps the
-  // IQ2_XXS arithmetic and the current tile's hand-off
-  {
-    int u = first(a.n_gu);
-    const int uend = base + a.n_gu;
-    if (u < uend && wait_once(a, kFlagRouted)) {
-      // experts and weights of every (token, slot) pair: lane p holds pair p
-      const int lane = threadIdx.x & 63;
-      const int P = a.T * K;  // <= kMaxDecodeT * 32 pairs; lanes hold the first 64
-      const int lp = min(lane, P - 1);
-      const int sel_l = ldc<true>(a.gu.selected + lp);
-      const float wgt_l = ldc<true>(a.gu.weights + lp);
-      auto pair_of = [&](int uu) { return (uu - base) / a.gu_tiles; };
-      auto expert_of = [&](int pair) {
-        const int e = pair < 64 ? __shfl(sel_l, pair, 64) : ldc<true>(a.gu.selected + pair);
-        return e < 0 ? 0 : e;
-      };
-      auto load = [&](int uu, uint32_t* wv) {
-        const DecodeArgs A = *decode_args();
-        const int tile = (uu - base) % A.gu_tiles, pair = pair_of(uu);
-        gu_load(A.gu, expert_of(pair), tile * A.gu.rows_per_wg, gu_item(A.gu, tile * A.gu.rows_per_wg, threadIdx.x), wv);
-      };
-      auto run = [&](int uu, const uint32_t* wv) {
-        const DecodeArgs A = *decode_args();
-        begin(A, uu);
-        const int idx = uu - base;
-        const int tile = idx % A.gu_tiles, pair = idx / A.gu_tiles, tok = pair / K, slot = pair - tok * K;
-        const int I = A.gu.I, R = A.gu.rows_per_wg, nbI = I / 256, blk = (tile * R) >> 8, row0 = tile * R;
-        const GuLds l = gu_lds(A.gu, smem);
-        const int want = 1 * 16 + tok;
-        if (tag != want) {
-          load_iq2_tables(l.tab);
-          stage_q8k<true>(A.gu.xq + (size_t)tok * (A.gu.d >> 8) * Q8K_BYTES, A.gu.d >> 8, l.q8, l.yd, nullptr);
-          tag = want;
-        }
-        __syncthreads();
-        if (A.trace && threadIdx.x == 0) A.trace[8 * uu + 4] = __builtin_amdgcn_s_memrealtime();
-        gu_compute(A.gu, gu_item(A.gu, row0, threadIdx.x), wv, l);
-        __syncthreads();
-        if (A.trace && threadIdx.x == 0) A.trace[8 * uu + 5] = __builtin_amdgcn_s_memrealtime();
-        const float wgt = pair < 64 ? __shfl(wgt_l, pair, 64) : ldc<true>(A.gu.weights + pair);
-        gu_epilogue<true>(A.gu, pair, row0, wgt, l);
-        if (A.trace && threadIdx.x == 0) A.trace[8 * uu + 6] = __builtin_amdgcn_s_memrealtime();
-        if (after_stores(&s_flag, [&] { return rows_arrive(A, A.midrows + pair * nbI + blk, I, row0, R); })) {
-          role_q8k<true, true>(A.midq, pair * nbI + blk, smem);
-          tag = -1;
-          if (after_stores(&s_flag, [&] {
-                return tree_arrive(A, A.tr_tokmid + tok * A.tr_tokmid_stride, K * nbI, slot * nbI + blk);
-              }))
-            publish(A, kFlagTok0 + tok);
-          if (A.trace && threadIdx.x == 0) A.trace[8 * uu + 7] = __builtin_amdgcn_s_memrealtime();
-        }
-        end(A, uu, 4);
-      };
-      uint32_t wa[33], wb[33];
-      load(u, wa);
-      while (true) {
-        int un = u + G;
-        if (un < uend) load(un, wb);
-        run(u, wa);
-        if (un >= uend) break;
-        u = un;
-        un = u + G;
-        if (un < uend) load(un, wa);
-        run(u, wb);
-        if (un >= uend) break;
-        u = un;
-      }
-    }
-  }
-  base += a.n_gu;
-  tag = -1;
-  for (int u = first(a.n_shdn); u < base + a.n_shdn; u += G) {
-    const DecodeArgs A = *decode_args();
-    begin(A, u);
-    const int w = u - base;
-    const int tile = w % A.shdn_tiles, tok = w / A.shdn_tiles;
-    auto ready = [&] { return wait_once(A, kFlagSh0 + tok); };
-    if (A.sh_fmt == 0) {
-      role_q80_matvec<true>(A.sh_dn, tile, tok, smem, ready, tag != 4 * 16 + tok);
-      tag = 4 * 16 + tok;
-    } else {
-      role_down<true>(A.sh_q2k, tile, tok, smem, ready, tag != 5 * 16 + tok);
-      tag = 5 * 16 + tok;
-    }
-    end(A, u, 5);
-  }
-  base += a.n_shdn;
-  tag = -1;
-  for (int u = first(a.n_dn); u < base + a.n_dn; u += G) {
-    const DecodeArgs A = *decode_args();
-    begin(A, u);
-    const int w = u - base;
-    const int tile = w % A.dn_tiles, tok = w / A.dn_tiles;
-    if (wait_once(A, kFlagRouted)) {
-      role_down<true>(A.dn, tile, tok, smem, [&] { return wait_once(A, kFlagTok0 + tok); }, tag != 3 * 16 + tok);
-      tag = 3 * 16 + tok;
-    }
-    end(A, u, 6);
-  }
 }
 
 // utils.rs:141-163

@@ -28,14 +28,12 @@ EXPORTED = [
     "dsmoe_scratch_bytes", "dsmoe_forward", "dsmoe_router_logits", "dsmoe_router_select",
     "dsmoe_q8k_quantize", "dsmoe_q8_0_quantize", "dsmoe_gate_up_mid", "dsmoe_down", "dsmoe_moe_sum",
     "dsmoe_q8_0_matvec", "dsmoe_swiglu", "dsmoe_dispatch", "dsmoe_tensor_bytes", "dsmoe_synth_tensor",
-    "dsmoe_synth_tensor_host", "dsmoe_stage_name", "dsmoe_set_profiling", "dsmoe_profile_read", "dsmoe_check", "dsmoe_set_option", "dsmoe_set_trace",
+    "dsmoe_synth_tensor_host", "dsmoe_stage_name", "dsmoe_set_profiling", "dsmoe_profile_read",
     "dsmoe_q8k_quantize_h", "dsmoe_gate_up_mid_sorted", "dsmoe_down_sorted", "dsmoe_q8_0_quantize_h",
     "dsmoe_q8_0_gemm",
 ]
 GROUPED_TILE_M = 64  # DSMOE_GROUPED_TILE_M
-STAGE_COUNT = 10
-OPT_FUSED_DECODE, OPT_DECODE_WGS_PER_CU, OPT_POLL_SLEEP, OPT_PERSISTENT_STAGES, OPT_HOLD_STREAMS = 0, 1, 2, 3, 4
-OPT_THREE_STAGE, OPT_INTERLEAVE, OPT_BLOCK_UP, OPT_BLOCK_DN, OPT_FUSE_MIDQ = 5, 6, 7, 8, 9
+STAGE_COUNT = 9
 
 
 class DsmoeError(RuntimeError):
@@ -85,8 +83,8 @@ def lib():
         "dsmoe_down_sorted": ([vp] * 9 + [i32] * 4 + [vp], i32),
         "dsmoe_q8_0_quantize_h": ([vp, vp, vp, vp, i32, i32, vp], i32),
         "dsmoe_q8_0_gemm": ([vp, vp, vp, vp, vp, i32, i32, i32, f32, vp], i32),
-        "dsmoe_gate_up_mid": ([vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, vp], i32),
-        "dsmoe_down": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, vp], i32),
+        "dsmoe_gate_up_mid": ([vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, vp], i32),
+        "dsmoe_down": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp], i32),
         "dsmoe_moe_sum": ([vp, vp, i32, i32, i32, vp], i32),
         "dsmoe_q8_0_matvec": ([vp, vp, vp, vp, i32, i32, i32, vp], i32),
         "dsmoe_swiglu": ([vp, vp, vp, i32, f32, f32, vp], i32),
@@ -94,9 +92,6 @@ def lib():
         "dsmoe_tensor_bytes": ([i32, i64, i32, i32], ctypes.c_size_t),
         "dsmoe_stage_name": ([i32], ctypes.c_char_p),
         "dsmoe_set_profiling": ([vp, i32], i32),
-        "dsmoe_check": ([vp, vp], i32),
-        "dsmoe_set_option": ([vp, i32, i32], i32),
-        "dsmoe_set_trace": ([vp, vp], i32),
         "dsmoe_profile_read": ([vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), i32], i32),
         "dsmoe_synth_tensor": ([vp, i32, u64, u64, i64, i32, i32, i32, i32, f32, vp], i32),
         "dsmoe_synth_tensor_host": ([vp, i32, u64, u64, i64, i32, i32, i32, i32, f32, i32], i32),
@@ -249,13 +244,16 @@ def q8_0_quantize(x, xq, xscale, in_dim, rows, stream=None):
     check(lib().dsmoe_q8_0_quantize(_p(x), _p(xq), _p(xscale), in_dim, rows, _stream(stream)))
 
 
-def gate_up_mid(gate, up, xq, selected, weights, gate_out, up_out, mid_out, d, I, T, k, clamp, stream=None):
+def gate_up_mid(gate, up, xq, selected, weights, gate_out, up_out, mid_out, d, I, T, k, E, clamp, stream=None):
+    """moe_gate_up_mid_qwarp32 (moe.rs:622-715); E = experts in gate/up (ids outside [0, E) read expert 0)."""
     check(lib().dsmoe_gate_up_mid(_p(gate), _p(up), _p(xq), _p(selected), _p(weights), _p(gate_out),
-                                  _p(up_out), _p(mid_out), d, I, T, k, clamp, _stream(stream)))
+                                  _p(up_out), _p(mid_out), d, I, T, k, E, clamp, _stream(stream)))
 
 
-def down(w, midq, selected, down_out, out, d, I, T, k, stream=None):
-    check(lib().dsmoe_down(_p(w), _p(midq), _p(selected), _p(down_out), _p(out), d, I, T, k, _stream(stream)))
+def down(w, midq, selected, down_out, out, d, I, T, k, E, stream=None):
+    """moe_down_qwarp32 + moe_sum (moe.rs:821-866, 983-1005); E as for gate_up_mid."""
+    check(lib().dsmoe_down(_p(w), _p(midq), _p(selected), _p(down_out), _p(out), d, I, T, k, E,
+                           _stream(stream)))
 
 
 def moe_sum(down_t, out, d, k, T, stream=None):
@@ -319,22 +317,6 @@ class MoeLayer:
     @property
     def scratch_bytes(self):
         return int(lib().dsmoe_scratch_bytes(self._ctx))
-
-    def set_trace(self, buf):
-        """Per-workgroup timeline of the decode launch into `buf` (int64, 4 per workgroup) or None."""
-        check(lib().dsmoe_set_trace(self._ctx, _p(buf)))
-
-    def set_fused_decode(self, on: bool):
-        """Run T <= 8 as one persistent launch, or as the staged launches (default)."""
-        check(lib().dsmoe_set_option(self._ctx, OPT_FUSED_DECODE, int(on)))
-
-    def set_option(self, option: int, value: int):
-        """dsmoe_set_option: OPT_FUSED_DECODE, OPT_DECODE_WGS_PER_CU, OPT_POLL_SLEEP."""
-        check(lib().dsmoe_set_option(self._ctx, int(option), int(value)))
-
-    def check(self, stream=None):
-        """Raise if a device-side dependency wait of the decode launch timed out."""
-        check(lib().dsmoe_check(self._ctx, _stream(stream)))
 
     def set_profiling(self, on: bool):
         check(lib().dsmoe_set_profiling(self._ctx, int(on)))

@@ -44,8 +44,7 @@ enum {
   DSMOE_ERR_UNSUPPORTED = 2, /* valid but outside what the kernels handle */
   DSMOE_ERR_HIP = 3,         /* HIP runtime error */
   DSMOE_ERR_NOMEM = 4,       /* device allocation failed */
-  DSMOE_ERR_MODULE = 5,      /* kernel code object missing / unloadable */
-  DSMOE_ERR_SYNC = 6         /* a device-side dependency wait timed out (dsmoe_check) */
+  DSMOE_ERR_MODULE = 5       /* kernel code object missing / unloadable */
 };
 
 /* Layer configuration.  The reference hard-codes d=4096, I=2048, E=256,
@@ -53,9 +52,9 @@ enum {
  * session.rs:21); here they are runtime parameters.  n_group = 1 is the
  * reference's routing; n_group > 1 adds group-limited top-k. */
 typedef struct dsmoe_config {
-  int32_t d_model;     /* multiple of 512 */
+  int32_t d_model;     /* multiple of 512, at most 8192 */
   int32_t d_ff;        /* routed expert intermediate, multiple of 256 */
-  int32_t n_expert;    /* 1..1024 */
+  int32_t n_expert;    /* 1..1024 (the batch path needs <= 512; above, every T runs the matvec launches) */
   int32_t top_k;       /* 1..32 */
   int32_t n_group;     /* 1 = reference routing; else divides n_expert, <= 64 */
   int32_t topk_group;  /* groups kept when n_group > 1 */
@@ -95,19 +94,16 @@ int dsmoe_destroy(dsmoe_ctx* ctx);
 /* Bytes of device scratch the context holds. */
 size_t dsmoe_scratch_bytes(const dsmoe_ctx* ctx);
 
-/* Waits for `stream` and reports whether any dsmoe_forward since the last
- * check abandoned a device-side dependency wait (DSMOE_ERR_SYNC; the flag is
- * then cleared).  No reference counterpart: the reference's launches have no
- * device-side waits.  The decode path (T <= 8) runs the layer as one launch
- * whose workgroups wait on each other with bounded spins. */
-int dsmoe_check(dsmoe_ctx* ctx, dsmoe_stream_t stream);
-
 /* The MoE FFN of one layer for T tokens (session.rs:1894-2155):
  *   x          f32 [T][d]   (ffn_norm)
  *   shared_out f32 [T][d]   shared expert output
  *   routed_out f32 [T][d]   sum over the k routed experts in slot order
  *   selected   i32 [T][k], weights f32 [T][k]: routing, optional (NULL)
- * hc_expand's input is shared_out + routed_out (session.rs:2157-2175). */
+ * hc_expand's input is shared_out + routed_out (session.rs:2157-2175).
+ * T <= 8 runs three launches (router logits + quantized x | routing, routed
+ * and shared gate/up and quantized mid | routed and shared down); larger T
+ * sorts the pairs by expert and runs grouped GEMMs.  Calls that overlap on
+ * one context race (they share its scratch and row counters). */
 int dsmoe_forward(dsmoe_ctx* ctx, const dsmoe_weights* w, const float* x, int32_t T,
                   float* shared_out, float* routed_out, int32_t* selected, float* weights,
                   dsmoe_stream_t stream);
@@ -123,7 +119,6 @@ enum {
   DSMOE_STAGE_UP,         /* routed + shared gate/up/SwiGLU               */
   DSMOE_STAGE_MIDQ,       /* activation quantization of the SwiGLU output */
   DSMOE_STAGE_DN,         /* routed down + slot sum + shared down         */
-  DSMOE_STAGE_DECODE,     /* the whole layer as one launch (T <= 8)       */
   /* inside UP / DN on the grouped path (T > 8) */
   DSMOE_STAGE_GU_GROUPED, /* routed gate/up/SwiGLU grouped GEMM            */
   DSMOE_STAGE_SH_UP,      /* shared gate/up/SwiGLU GEMM                    */
@@ -134,55 +129,6 @@ enum {
 const char* dsmoe_stage_name(int32_t stage);
 int dsmoe_set_profiling(dsmoe_ctx* ctx, int32_t enable);
 int dsmoe_profile_read(dsmoe_ctx* ctx, double* total_ms, int64_t* launches, int32_t reset);
-
-/* Context options (no reference counterpart).  The staged decode path is
- * prep | routing | gate/up | mid quantization | down; by default the routing
- * and the mid quantization run inside the gate/up launch (three launches),
- * the options below split them out or change the launch shapes.
- *   DSMOE_OPT_FUSED_DECODE (default 0): 1 runs T <= 8 as the single
- *   persistent launch, 0 the staged path (same results).
- *   DSMOE_OPT_DECODE_WGS_PER_CU (default 0 = as many as fit): cap on the
- *   persistent launch's workgroups per compute unit.  The persistent launch
- *   needs all of its workgroups resident at once: it is sized from the
- *   occupancy of an otherwise idle GPU, and a dependency wait that cannot
- *   end (the GPU shared with other work) is reported by dsmoe_check.
- *   DSMOE_OPT_POLL_SLEEP (default 2): pause between two polls of a
- *   dependency flag, in units of 64 GPU clocks.
- *   DSMOE_OPT_PERSISTENT_STAGES (default 0): 1 = the staged path's
- *   gate/up and down launches for T <= 8 run as persistent grids with the
- *   next work unit's weights in flight (same results).
- *   DSMOE_OPT_HOLD_STREAMS (default 0): 1 = in the one-launch decode path the
- *   shared-expert streams start after the routing instead of alongside it.
- *   DSMOE_OPT_THREE_STAGE (default 0): 1 = T <= 8 with a Q8_0 (or no)
- *   shared expert runs in three launches (routing + shared gate/up | routed
- *   gate/up + shared down | routed down) instead of the staged path.  Same
- *   results.
- *   DSMOE_OPT_INTERLEAVE (default 0): staged path; bit 0 alternates
- *   routed and shared workgroups in the gate/up launch, bit 1 in the down
- *   launch; bit 2 / bit 3 dispatch the shared workgroups first in the
- *   gate/up / down launch (dispatch order only; same results).
- *   DSMOE_OPT_BLOCK_UP / DSMOE_OPT_BLOCK_DN (default 0): 0 = the staged
- *   path's gate/up and down launches in the row-streaming form (a few lanes
- *   per weight row, each lane streaming its blocks of the row; used where
- *   the shapes fit: d <= 8192, and k <= 8 with d_ff <= 2048 for the down
- *   launch), 256 / 512 / 1024 = the per-item form (one block pair or block
- *   per thread) with workgroups of at most that many threads.  Same results.
- *   DSMOE_OPT_FUSE_MIDQ (default 1): the row-streaming gate/up launch also
- *   quantizes the mid rows (the workgroup completing each 256-row block does
- *   it; no waiting), so decode is three launches; 0 = a launch of its own.
- *   Applies with a Q8_0 (or no) shared expert.  Same results. */
-enum { DSMOE_OPT_FUSED_DECODE = 0, DSMOE_OPT_DECODE_WGS_PER_CU = 1, DSMOE_OPT_POLL_SLEEP = 2,
-       DSMOE_OPT_PERSISTENT_STAGES = 3, DSMOE_OPT_HOLD_STREAMS = 4, DSMOE_OPT_THREE_STAGE = 5,
-       DSMOE_OPT_INTERLEAVE = 6, DSMOE_OPT_BLOCK_UP = 7, DSMOE_OPT_BLOCK_DN = 8, DSMOE_OPT_FUSE_MIDQ = 9 };
-int dsmoe_set_option(dsmoe_ctx* ctx, int32_t option, int32_t value);
-
-/* Timeline of the one-launch decode path (no reference counterpart): when
- * `buf` (device, 8 x u64 per work unit of the launch; at most 16384 units)
- * is set, every unit records {start, end of its last dependency wait, end,
-
- * role << 32 | hardware id, then role-specific stamps} on the GPU's constant 100 MHz clock.  NULL
- * disables it. */
-int dsmoe_set_trace(dsmoe_ctx* ctx, void* buf);
 
 /* --------------------------------------------------------------------- */
 /* Per-kernel entry points (the reference launch surface)                 */
@@ -219,10 +165,13 @@ int dsmoe_q8_0_quantize(const float* x, int8_t* xq, float* xscale, int32_t in_di
 
 /* moe_gate_up_mid_qwarp32 (engine/src/kernels/moe.rs:622-715): for pair =
  * t*k + slot and row < I, gate/up = IQ2_XXS row . Q8_K x[t], clamped;
- * mid = silu(gate) * up * weights[pair].  gate_out/up_out may be NULL. */
+ * mid = silu(gate) * up * weights[pair].  gate_out/up_out may be NULL.
+ * E = experts in gate/up: an id outside [0, E) reads expert 0 (the
+ * reference's -1 for an unfilled slot does the same; it checks no upper
+ * bound).  selected NULL = expert 0 for every pair, weights NULL = 1. */
 int dsmoe_gate_up_mid(const void* gate, const void* up, const void* xq, const int32_t* selected,
                       const float* weights, float* gate_out, float* up_out, float* mid_out, int32_t d,
-                      int32_t I, int32_t T, int32_t k, float clamp, dsmoe_stream_t stream);
+                      int32_t I, int32_t T, int32_t k, int32_t E, float clamp, dsmoe_stream_t stream);
 
 /* moe_gate_up_mid_sorted_qwarp32 (engine/src/kernels/moe.rs:721-815):
  * the pairs grouped by expert by dsmoe_dispatch with block_m =
@@ -249,14 +198,16 @@ int dsmoe_down_sorted(const void* down, const uint16_t* mh, const void* mq, cons
 
 /* moe_down_qwarp32 + moe_sum / moe_down_sum6_qwarp32 (engine/src/kernels/
  * moe.rs:821-866, :922-1005): down_out[pair][row] = Q2_K row . Q8_K
- * midq[pair]; out[t][row] = slot-ordered sum.  Either output may be NULL. */
+ * midq[pair]; out[t][row] = slot-ordered sum.  Either output may be NULL.
+ * E and ids outside [0, E) as for dsmoe_gate_up_mid. */
 int dsmoe_down(const void* down, const void* midq, const int32_t* selected, float* down_out, float* out,
-               int32_t d, int32_t I, int32_t T, int32_t k, dsmoe_stream_t stream);
+               int32_t d, int32_t I, int32_t T, int32_t k, int32_t E, dsmoe_stream_t stream);
 
 /* moe_sum (engine/src/kernels/moe.rs:983-1005). */
 int dsmoe_moe_sum(const float* down, float* out, int32_t d, int32_t k, int32_t T, dsmoe_stream_t stream);
 
-/* matmul_q8_0_preq_warp8 / _batch_warp8 (engine/src/kernels/matmul.rs:357-458). */
+/* matmul_q8_0_preq_warp8 / _batch_warp8 (engine/src/kernels/matmul.rs:357-458).
+ * in_dim a multiple of 64. */
 int dsmoe_q8_0_matvec(const void* w, const int8_t* xq, const float* xscale, float* out, int32_t in_dim,
                       int32_t out_dim, int32_t T, dsmoe_stream_t stream);
 

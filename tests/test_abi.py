@@ -32,7 +32,7 @@ def test_code_object_built():
     blob = open(dsmoe.CODE_OBJECT_PATH, "rb").read()
     assert b"gfx950" in blob
     for k in ("dsmoe_prep", "dsmoe_up", "dsmoe_dn", "dsmoe_up_rows", "dsmoe_dn_rows", "dsmoe_midq",
-              "dsmoe_router_select", "dsmoe_dispatch", "dsmoe_decode"):
+              "dsmoe_router_select", "dsmoe_dispatch", "dsmoe_moe_sum", "dsmoe_swiglu", "dsmoe_synth"):
         assert k.encode() in blob
     gemm = os.path.join(os.path.dirname(dsmoe.CODE_OBJECT_PATH), "dsmoe_gemm.hsaco")
     blob = open(gemm, "rb").read()
@@ -69,10 +69,11 @@ def test_stage_entry_points_validate_before_launch():
     fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     assert L.dsmoe_router_logits(nul, fake, fake, 7168, 256, 1, nul) == 1
     assert L.dsmoe_q8k_quantize(fake, fake, 300, 1, nul) == 1
-    assert L.dsmoe_gate_up_mid(fake, fake, fake, fake, fake, nul, nul, fake, 7168 + 256, 2048, 1, 8, 10.0, nul) == 2
-    assert L.dsmoe_gate_up_mid(ctypes.c_void_p(0x1004), fake, fake, fake, fake, nul, nul, fake, 7168, 2048, 1, 8, 10.0, nul) == 1
-    assert L.dsmoe_down(fake, fake, fake, nul, nul, 7168, 2048, 1, 8, nul) == 1
-    assert L.dsmoe_down(fake, fake, fake, nul, fake, 7168, 2000, 1, 8, nul) == 1
+    assert L.dsmoe_gate_up_mid(fake, fake, fake, fake, fake, nul, nul, fake, 7168 + 256, 2048, 1, 8, 256, 10.0, nul) == 2
+    assert L.dsmoe_gate_up_mid(ctypes.c_void_p(0x1004), fake, fake, fake, fake, nul, nul, fake, 7168, 2048, 1, 8, 256, 10.0, nul) == 1
+    assert L.dsmoe_down(fake, fake, fake, nul, nul, 7168, 2048, 1, 8, 256, nul) == 1
+    assert L.dsmoe_down(fake, fake, fake, nul, fake, 7168, 2000, 1, 8, 256, nul) == 1
+    assert L.dsmoe_down(fake, fake, fake, nul, fake, 7168, 2048, 1, 8, 0, nul) == 1  # E < 1
     assert L.dsmoe_dispatch(fake, 10, 600, 16, fake, fake, fake, nul, nul, nul, nul) == 2
     assert L.dsmoe_q8_0_matvec(fake, fake, fake, fake, 100, 10, 1, nul) == 2
     c = _cfg(n_expert=2000).c()

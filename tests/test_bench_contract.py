@@ -22,13 +22,15 @@ def test_more_than_one_gpu_is_refused():
     assert "one GPU" in r.stderr and r.stdout == ""
 
 
-def test_roofline_traffic_comes_from_the_committed_profiles():
+def test_roofline_traffic_is_tied_to_the_code_object(tmp_path):
+    """A traffic line counts only for the code object it was measured on."""
     b = _bench()
-    up = b.measured_traffic(b.STAGE_KERNEL["up"], "c2", "staged")
-    gu = b.measured_traffic(b.PREFILL_KERNEL["gu_grouped"], "c5", "grouped")
-    assert up is not None and gu is not None
-    # HBM bytes per launch at least the algorithmic weight bytes (91.8 MB of
-    # gate/up weights at c2 decode; 1.9 GB of routed gate/up weights at c5)
-    assert 91_824_128 <= up < 2 * 91_824_128
-    assert 1_900_000_000 <= gu
-    assert b.measured_traffic("no_such_kernel", "c2", "staged") is None
+    h = b.code_object_hash("dsmoe_up_rows")
+    assert h is not None and len(h) == 16
+    assert b.code_object_hash("dsmoe_gu_grouped") != h
+    f = tmp_path / "moe_decode_c2_traffic.txt"
+    f.write_text(f"traffic kernel=dsmoe_up_rows config=c2 path=staged bytes=123 code_object={h}\n"
+                 f"traffic kernel=dsmoe_dn_rows config=c2 path=staged bytes=456 code_object=0123456789abcdef\n")
+    assert b.measured_traffic("dsmoe_up_rows", "c2", "staged", str(tmp_path)) == 123
+    assert b.measured_traffic("dsmoe_dn_rows", "c2", "staged", str(tmp_path)) is None  # stale
+    assert b.measured_traffic("dsmoe_prep", "c2", "staged", str(tmp_path)) is None  # not measured

@@ -155,12 +155,12 @@ def test_gate_up_down_bitexact(gpu, d, I, E, T, k):
     g = torch.empty(P_, I, device=gpu)
     u = torch.empty(P_, I, device=gpu)
     m = torch.empty(P_, I, device=gpu)
-    dsmoe.gate_up_mid(gate, up, xq, dsel, dw, g, u, m, d, I, T, k, 10.0)
+    dsmoe.gate_up_mid(gate, up, xq, dsel, dw, g, u, m, d, I, T, k, E, 10.0)
     mq = torch.empty(P_ * (I // 256) * 292, dtype=torch.uint8, device=gpu)
     dsmoe.q8k_quantize(m, mq, I, P_)
     dd = torch.empty(P_, d, device=gpu)
     ro = torch.empty(T, d, device=gpu)
-    dsmoe.down(dn, mq, dsel, dd, ro, d, I, T, k)
+    dsmoe.down(dn, mq, dsel, dd, ro, d, I, T, k, E)
     ro2 = torch.empty(T, d, device=gpu)
     dsmoe.moe_sum(dd, ro2, d, k, T)
     torch.cuda.synchronize()
@@ -184,6 +184,44 @@ def test_gate_up_down_bitexact(gpu, d, I, E, T, k):
     L.or_moe_sum(O.P(d0), O.P(s0), d, k, T)
     assert_close(np_(ro).reshape(-1), s0, "down slot sum")
     assert bits_equal(np_(ro2), np_(ro))
+
+
+@pytest.mark.parametrize("d,I,E,T,k", [(7168, 2048, 8, 3, 8), (2048, 1024, 6, 2, 4), (1024, 4096, 12, 1, 10)])
+def test_expert_ids_outside_range_read_expert_0(gpu, d, I, E, T, k):
+    """gate_up_mid / down with ids -1, E, E + 5 and 2^31 - 1 in `selected`:
+    those slots read expert 0 (the weights hold exactly E experts, so an
+    unclamped id would read past the allocation) and give the bits of the
+    same call with 0 in their place."""
+    import torch
+    say(f"ids outside [0,E) d={d} I={I} E={E} T={T} k={k}")
+    gate = dsmoe.synth(dsmoe.FMT_IQ2_XXS, 3, 1, E, I, d, sigma=0.02, device=gpu)
+    up = dsmoe.synth(dsmoe.FMT_IQ2_XXS, 3, 2, E, I, d, sigma=0.02, device=gpu)
+    dn = dsmoe.synth(dsmoe.FMT_Q2_K, 3, 3, E, d, I, sigma=0.02, device=gpu)
+    x = dsmoe.synth(dsmoe.FMT_F32, 3, 4, 1, T, d, sigma=1.0, device=gpu)
+    rng = np.random.default_rng(E * 7 + T)
+    sel = rng.integers(0, E, size=(T, k)).astype(np.int32)
+    bad = np.array([-1, E, E + 5, 2**31 - 1], np.int32)
+    pos = rng.choice(T * k, size=min(T * k, 6), replace=False)
+    sel.reshape(-1)[pos] = bad[np.arange(len(pos)) % 4]
+    fixed = np.where((sel < 0) | (sel >= E), 0, sel).astype(np.int32)
+    w = rng.random((T, k), dtype=np.float32)
+    xq = torch.empty(T * (d // 256) * 292, dtype=torch.uint8, device=gpu)
+    dsmoe.q8k_quantize(x, xq, d, T)
+    dw = torch.from_numpy(w.reshape(-1)).to(gpu)
+    outs = []
+    for s in (sel, fixed):
+        dsel = torch.from_numpy(s.reshape(-1).copy()).to(gpu)
+        m = torch.empty(T * k, I, device=gpu)
+        dsmoe.gate_up_mid(gate, up, xq, dsel, dw, None, None, m, d, I, T, k, E, 10.0)
+        mq = torch.empty(T * k * (I // 256) * 292, dtype=torch.uint8, device=gpu)
+        dsmoe.q8k_quantize(m, mq, I, T * k)
+        dd = torch.empty(T * k, d, device=gpu)
+        ro = torch.empty(T, d, device=gpu)
+        dsmoe.down(dn, mq, dsel, dd, ro, d, I, T, k, E)
+        torch.cuda.synchronize()
+        outs.append([np_(m), np_(dd), np_(ro)])
+    for a, b in zip(*outs):
+        assert bits_equal(a, b)
 
 
 def _iq2_big_blocks(rng, n_blocks):
@@ -230,7 +268,7 @@ def test_gate_up_sorted_matches_per_pair(gpu, d, I, E, T, k, skew, big):
     m_ref = torch.empty(P_, I, device=gpu)
     g_ = torch.empty(P_, I, device=gpu)
     u_ = torch.empty(P_, I, device=gpu)
-    dsmoe.gate_up_mid(gate, up, xq, dsel, dw, g_, u_, m_ref, d, I, T, k, 10.0)
+    dsmoe.gate_up_mid(gate, up, xq, dsel, dw, g_, u_, m_ref, d, I, T, k, E, 10.0)
     u32 = dict(dtype=torch.int32, device=gpu)
     counts, offsets = torch.empty(E, **u32), torch.empty(E + 1, **u32)
     sp = torch.empty(P_, **u32)
@@ -253,7 +291,7 @@ def test_gate_up_sorted_matches_per_pair(gpu, d, I, E, T, k, skew, big):
     dsmoe.q8k_quantize_h(m_ref, mq, mh, I, P_)
     dd_ref = torch.empty(P_, d, device=gpu)
     ro = torch.empty(T, d, device=gpu)
-    dsmoe.down(dn, mq, dsel, dd_ref, ro, d, I, T, k)
+    dsmoe.down(dn, mq, dsel, dd_ref, ro, d, I, T, k, E)
     dd = torch.full((P_, d), float("nan"), device=gpu)
     dsmoe.down_sorted(dn, mh, mq, sp, offsets, toff, texp, tst, dd, d, I, E, P_)
     torch.cuda.synchronize()
@@ -418,47 +456,28 @@ def test_layer_c5_zipf_sampled(gpu):
     assert top10 > 0.5
 
 
-@pytest.mark.parametrize("name,Ts", [("c1", [1, 3, 8]), ("c2", [1, 2, 8])])
-def test_fused_decode_equals_staged(gpu, name, Ts):
-    """The one-launch decode path (device-side hand-offs) must produce the
-    staged path's bits, call after call (its counters reset themselves)."""
+@pytest.mark.parametrize("name,Ts", [("c1", [1, 3, 8, 5]), ("c2", [1, 2, 8])])
+def test_decode_calls_in_a_row(gpu, name, Ts):
+    """One context, decode calls of varying T in a row: every call matches the
+    oracle (the completion counters of the selection and of the mid
+    quantization reset themselves between launches)."""
     import torch
     case = C.CASES[name]
     w = C.make_weights(case, device=gpu)
+    hw = _host_weights(w)
     d, k = case.cfg.d_model, case.cfg.top_k
-    fused = dsmoe.MoeLayer(case.cfg, 8)
-    fused.set_fused_decode(True)
-    staged = dsmoe.MoeLayer(case.cfg, 8)  # default: row-streaming launches, mid quantized in the gate/up launch
-    three = dsmoe.MoeLayer(case.cfg, 8)   # three launches
-    three.set_option(dsmoe.OPT_THREE_STAGE, 1)
-    pers = dsmoe.MoeLayer(case.cfg, 8)    # staged, persistent gate/up and down
-    pers.set_option(dsmoe.OPT_PERSISTENT_STAGES, 1)
-    inter = dsmoe.MoeLayer(case.cfg, 8)   # staged, routed and shared workgroups alternating
-    inter.set_option(dsmoe.OPT_INTERLEAVE, 3)
-    first = dsmoe.MoeLayer(case.cfg, 8)   # staged, shared workgroups dispatched first
-    first.set_option(dsmoe.OPT_INTERLEAVE, 12)
-    item = dsmoe.MoeLayer(case.cfg, 8)    # staged, per-item gate/up and down
-    item.set_option(dsmoe.OPT_BLOCK_UP, 256)
-    item.set_option(dsmoe.OPT_BLOCK_DN, 1024)
-    sepq = dsmoe.MoeLayer(case.cfg, 8)    # row-streaming, mid quantization as a launch of its own
-    sepq.set_option(dsmoe.OPT_FUSE_MIDQ, 0)
-    layers = (fused, staged, three, pers, inter, first, item, sepq)
+    lay = dsmoe.MoeLayer(case.cfg, 8)
     for rep, T in enumerate(Ts * 2):
-        say(f"decode paths (fused, default, three-launch, persistent, interleaved, shared-first, per-item, "
-            f"separate midq) "
-            f"{name} T={T} rep={rep}")
+        say(f"decode calls {name} T={T} rep={rep}")
         x = C.make_x(case, T=T, step=rep, device=gpu)
-        outs = []
-        for lay in layers:
-            so = torch.full((T, d), float("nan"), device=gpu)
-            ro = torch.full((T, d), float("nan"), device=gpu)
-            sel = torch.full((T, k), -7, dtype=torch.int32, device=gpu)
-            wt = torch.full((T, k), float("nan"), device=gpu)
-            lay.forward(w, x, so, ro, sel, wt)
-            lay.check()
-            outs.append([np_(t) for t in (so, ro, sel, wt)])
-        for vals in zip(*outs):
-            for v in vals[1:]:
-                assert bits_equal(vals[0], v)
-    for lay in layers:
-        lay.close()
+        so = torch.full((T, d), float("nan"), device=gpu)
+        ro = torch.full((T, d), float("nan"), device=gpu)
+        sel = torch.full((T, k), -7, dtype=torch.int32, device=gpu)
+        wt = torch.full((T, k), float("nan"), device=gpu)
+        lay.forward(w, x, so, ro, sel, wt)
+        torch.cuda.synchronize()
+        so0, ro0, sel0, wt0 = O.moe_forward(case.cfg, hw, np_(x), T, NT)
+        assert np.array_equal(np_(sel), sel0)
+        assert bits_equal(np_(wt), wt0)
+        assert bits_equal(np_(ro), ro0) and bits_equal(np_(so), so0), f"call {rep} differs from the oracle"
+    lay.close()
