@@ -35,9 +35,13 @@ def build_code_object():
 
 def build_host():
     out = os.path.join(LIB, "libdsmoe.so")
+    # the static scratch of dsmoe_forward_noalloc: device code inside the library
+    obj = os.path.join(LIB, "dsmoe_noalloc.o")
+    run([os.path.join(ROCM, "bin", "hipcc"), "-c", "-fPIC", *HIP_FLAGS, os.path.join(CSRC, "dsmoe_noalloc.hip"),
+         "-o", obj])
     run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-ffp-contract=off", "-Wall",
          "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"),
-         "-I", CSRC, os.path.join(CSRC, "dsmoe_host.cpp"), "-o", out,
+         "-I", CSRC, os.path.join(CSRC, "dsmoe_host.cpp"), obj, "-o", out,
          "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath," + os.path.join(ROCM, "lib"),
          "-ldl", "-lpthread"])
     return out

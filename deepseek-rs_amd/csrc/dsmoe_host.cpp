@@ -17,6 +17,7 @@
 #include <mutex>
 #include <string>
 #include <thread>
+#include <type_traits>
 #include <vector>
 
 #include "dsmoe_formats.h"
@@ -94,12 +95,16 @@ const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_u
 const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1};
 static_assert(DSMOE_GROUPED_TILE_M == kGuBM, "header and kernels disagree on the grouped tile");
 
+extern "C" int dsmoe_noalloc_setup(void** ptr, size_t* bytes);  // dsmoe_noalloc.hip
+
 struct DeviceState {
   bool loaded = false;
   hipModule_t mod = nullptr;
   hipModule_t mod_gemm = nullptr;
   hipFunction_t fn[K_COUNT] = {};
   uint8_t* d_lvlmap = nullptr;
+  uint8_t* noalloc = nullptr;  // this device's static scratch (dsmoe_noalloc.hip)
+  size_t noalloc_bytes = 0;
 };
 
 constexpr int kMaxDevices = 64;
@@ -138,6 +143,13 @@ int load_device(const char* path, DeviceState** out) {
         return fail(DSMOE_ERR_MODULE, std::string("hipModuleGetFunction(") + kKernNames[k] + "): " +
                                           hipGetErrorString(e));
     }
+    void* sp = nullptr;
+    size_t sb = 0;
+    const int se = dsmoe_noalloc_setup(&sp, &sb);
+    if (se != 0)
+      return fail(DSMOE_ERR_HIP, std::string("static scratch set-up: ") + hipGetErrorString((hipError_t)se));
+    st.noalloc = (uint8_t*)sp;
+    st.noalloc_bytes = sb;
     st.loaded = true;
   }
   *out = &st;
@@ -679,14 +691,50 @@ int dsmoe_profile_read(dsmoe_ctx* c, double* total_ms, int64_t* launches, int32_
   return DSMOE_OK;
 }
 
+}  // extern "C"
+
+// Lays the matvec-path buffers of T tokens out from `base` (256-byte
+// aligned, each rounded up to 256 bytes) and sets c's pointers to them;
+// with base == nullptr only the size is computed.  Returns the bytes used.
+static int layer_fits_lds(const dsmoe_config& cf) {
+  if (gate_up_lds(cf.d_model / 256, 1) > 64 * 1024 || down_lds(cf.top_k, cf.d_ff / 256, 1) > 64 * 1024 ||
+      (cf.shared_fmt == 0 && (q80_lds(cf.d_model / 32, 2, 1) > 64 * 1024 || q80_lds(cf.d_ff_shared / 32, 1, 1) > 64 * 1024)))
+    return fail(DSMOE_ERR_UNSUPPORTED, "layer shape exceeds one workgroup's LDS");
+  return DSMOE_OK;
+}
+
+static size_t carve_matvec(dsmoe_ctx* c, const dsmoe_config& cf, size_t T, uint8_t* base) {
+  const size_t K = cf.top_k, E = cf.n_expert, d = cf.d_model, I = cf.d_ff, Is = std::max(cf.d_ff_shared, 256);
+  size_t at = 0;
+  auto C = [&](auto** p, size_t b) {
+    using Ptr = std::remove_reference_t<decltype(*p)>;
+    if (base) *p = (Ptr)(base + at);
+    at += (std::max<size_t>(b, 16) + 255) & ~(size_t)255;
+  };
+  C(&c->logits, T * E * 4);
+  C(&c->selected, T * K * 4);
+  C(&c->weights, T * K * 4);
+  C(&c->xq8k, T * (d / 256) * Q8K_BYTES);
+  C(&c->xq80, T * d);
+  C(&c->xs80, T * (d / 32) * 4);
+  C(&c->mid, T * K * I * 4);
+  C(&c->midq, T * K * (I / 256) * Q8K_BYTES);
+  C(&c->sh_mid, T * Is * 4);
+  C(&c->sh_midq, T * (Is / 256 + 1) * Q8K_BYTES);
+  C(&c->sh_q80, T * Is);
+  C(&c->sh_s80, T * (Is / 32 + 1) * 4);
+  C(&c->mid_cnt, ((size_t)kMaxDecodeT * K * (I / 256) + (size_t)kMaxDecodeT * ((Is + 255) / 256)) * 4);
+  return at;
+}
+
+extern "C" {
+
 int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
   if (!out) return fail(DSMOE_ERR_INVALID, "create: out is NULL");
   *out = nullptr;
   DSM_TRY(validate_cfg(cfg));
   if (max_tokens < 1) return fail(DSMOE_ERR_INVALID, "create: max_tokens must be >= 1");
-  if (gate_up_lds(cfg->d_model / 256, 1) > 64 * 1024 || down_lds(cfg->top_k, cfg->d_ff / 256, 1) > 64 * 1024 ||
-      (cfg->shared_fmt == 0 && (q80_lds(cfg->d_model / 32, 2, 1) > 64 * 1024 || q80_lds(cfg->d_ff_shared / 32, 1, 1) > 64 * 1024)))
-    return fail(DSMOE_ERR_UNSUPPORTED, "create: layer shape exceeds one workgroup's LDS");
+  DSM_TRY(layer_fits_lds(*cfg));
   DeviceState* st = nullptr;
   DSM_TRY(load_device(nullptr, &st));
   dsmoe_ctx* c = new dsmoe_ctx();
@@ -697,18 +745,13 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
   const size_t d = cfg->d_model, I = cfg->d_ff, Is = std::max(cfg->d_ff_shared, 256);
   int rc = DSMOE_OK;
   auto A = [&](auto** p, size_t b) { if (rc == DSMOE_OK) rc = ctx_alloc(c, p, b); };
-  A(&c->logits, T * E * 4);
-  A(&c->selected, T * K * 4);
-  A(&c->weights, T * K * 4);
-  A(&c->xq8k, T * (d / 256) * Q8K_BYTES);
-  A(&c->xq80, T * d);
-  A(&c->xs80, T * (d / 32) * 4);
-  A(&c->mid, T * K * I * 4);
-  A(&c->midq, T * K * (I / 256) * Q8K_BYTES);
-  A(&c->sh_mid, T * Is * 4);
-  A(&c->sh_midq, T * (Is / 256 + 1) * Q8K_BYTES);
-  A(&c->sh_q80, T * Is);
-  A(&c->sh_s80, T * (Is / 32 + 1) * 4);
+  uint8_t* base = nullptr;
+  const size_t nbytes = carve_matvec(c, *cfg, T, nullptr);
+  A(&base, nbytes);
+  if (rc == DSMOE_OK) {
+    carve_matvec(c, *cfg, T, base);
+    if (hipMemset(base, 0, nbytes) != hipSuccess) rc = fail(DSMOE_ERR_HIP, "create: hipMemset of the scratch failed");
+  }
   if (max_tokens > kDecodeMaxT && E <= 512) {
     const size_t P = T * K, max_tiles = P / kGuBM + std::min(E, P);
     A(&c->xh, T * d * 2);
@@ -722,12 +765,6 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
     A(&c->g_tile_offsets, (E + 1) * 4);
     A(&c->g_tile_experts, max_tiles * 4);
     A(&c->g_tile_starts, max_tiles * 4);
-  }
-  {
-    const size_t words = (size_t)kMaxDecodeT * K * (I / 256) + (size_t)kMaxDecodeT * ((Is + 255) / 256);
-    A(&c->mid_cnt, words * 4);
-    if (rc == DSMOE_OK && hipMemset(c->mid_cnt, 0, words * 4) != hipSuccess)
-      rc = fail(DSMOE_ERR_HIP, "create: hipMemset of the mid row counters failed");
   }
   if (rc != DSMOE_OK) {
     std::string msg = g_err;
@@ -753,7 +790,7 @@ int dsmoe_destroy(dsmoe_ctx* c) {
 
 size_t dsmoe_scratch_bytes(const dsmoe_ctx* c) { return c ? c->bytes : 0; }
 
-int dsmoe_forward(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t T, float* shared_out,
+static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t T, float* shared_out,
                   float* routed_out, int32_t* selected, float* weights, dsmoe_stream_t stream) {
   if (!c || !w || !x || !routed_out) return fail(DSMOE_ERR_INVALID, "forward: null pointer");
   if (T < 0 || T > c->max_tokens) return fail(DSMOE_ERR_INVALID, "forward: T outside 0..max_tokens");
@@ -904,6 +941,32 @@ int dsmoe_forward(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t 
                    dim3(rows ? 256 : std::max(s1.block, s2.block)), lds, stream, a));
   }
   return DSMOE_OK;
+}
+
+int dsmoe_forward(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t T, float* shared_out,
+                  float* routed_out, int32_t* selected, float* weights, dsmoe_stream_t stream) {
+  return forward_impl(c, w, x, T, shared_out, routed_out, selected, weights, stream);
+}
+
+int dsmoe_forward_noalloc(const dsmoe_config* cfg, const dsmoe_weights* w, const float* x, int32_t T,
+                          float* shared_out, float* routed_out, int32_t* selected, float* weights,
+                          dsmoe_stream_t stream) {
+  DSM_TRY(validate_cfg(cfg));
+  if (T < 0 || T > kDecodeMaxT) return fail(DSMOE_ERR_UNSUPPORTED, "forward_noalloc: T must be in 0..8");
+  DSM_TRY(layer_fits_lds(*cfg));
+  DeviceState* st = nullptr;
+  DSM_TRY(load_device(nullptr, &st));
+  dsmoe_ctx c;  // pointers into the static scratch; owns nothing
+  c.cfg = *cfg;
+  c.max_tokens = kDecodeMaxT;
+  c.device = -1;
+  const size_t need = carve_matvec(&c, *cfg, kDecodeMaxT, nullptr);
+  if (need > st->noalloc_bytes)
+    return fail(DSMOE_ERR_UNSUPPORTED, "forward_noalloc: the layer needs " + std::to_string(need) +
+                                           " bytes of scratch; the static buffer holds " +
+                                           std::to_string(st->noalloc_bytes));
+  carve_matvec(&c, *cfg, kDecodeMaxT, st->noalloc);
+  return forward_impl(&c, w, x, T, shared_out, routed_out, selected, weights, stream);
 }
 
 // --------------------------------------------------------------------------

@@ -25,7 +25,7 @@ IQ2XXS_BYTES, Q2K_BYTES, Q8K_BYTES, Q8_0_BYTES = 66, 84, 292, 34
 
 EXPORTED = [
     "dsmoe_version", "dsmoe_last_error", "dsmoe_init", "dsmoe_create", "dsmoe_destroy",
-    "dsmoe_scratch_bytes", "dsmoe_forward", "dsmoe_router_logits", "dsmoe_router_select",
+    "dsmoe_scratch_bytes", "dsmoe_forward", "dsmoe_forward_noalloc", "dsmoe_router_logits", "dsmoe_router_select",
     "dsmoe_q8k_quantize", "dsmoe_q8_0_quantize", "dsmoe_gate_up_mid", "dsmoe_down", "dsmoe_moe_sum",
     "dsmoe_q8_0_matvec", "dsmoe_swiglu", "dsmoe_dispatch", "dsmoe_tensor_bytes", "dsmoe_synth_tensor",
     "dsmoe_synth_tensor_host", "dsmoe_stage_name", "dsmoe_set_profiling", "dsmoe_profile_read",
@@ -74,6 +74,7 @@ def lib():
         "dsmoe_destroy": ([vp], i32),
         "dsmoe_scratch_bytes": ([vp], ctypes.c_size_t),
         "dsmoe_forward": ([vp, ctypes.POINTER(Weights), vp, i32, vp, vp, vp, vp, vp], i32),
+        "dsmoe_forward_noalloc": ([ctypes.POINTER(Config), ctypes.POINTER(Weights), vp, i32, vp, vp, vp, vp, vp], i32),
         "dsmoe_router_logits": ([vp, vp, vp, i32, i32, i32, vp], i32),
         "dsmoe_router_select": ([ctypes.POINTER(Config), vp, vp, i32, vp, vp, vp, vp], i32),
         "dsmoe_q8k_quantize": ([vp, vp, i32, i32, vp], i32),
@@ -291,6 +292,14 @@ class LayerWeights:
     def c(self) -> Weights:
         return Weights(*[(_p(getattr(self, n)).value or None) for n in
                          ("router_f16", "bias", "gate", "up", "down", "sh_gate", "sh_up", "sh_down")])
+
+
+def forward_noalloc(cfg, w, x, shared_out, routed_out, selected=None, weights=None, stream=None):
+    """dsmoe_forward_noalloc: one decode call (T <= 8) on the static device
+    scratch, with no context and no allocation; calls that overlap on one GPU race."""
+    c, wc = cfg.c(), w.c()
+    check(lib().dsmoe_forward_noalloc(ctypes.byref(c), ctypes.byref(wc), _p(x), x.shape[0], _p(shared_out),
+                                      _p(routed_out), _p(selected), _p(weights), _stream(stream)))
 
 
 class MoeLayer:

@@ -108,6 +108,19 @@ int dsmoe_forward(dsmoe_ctx* ctx, const dsmoe_weights* w, const float* x, int32_
                   float* shared_out, float* routed_out, int32_t* selected, float* weights,
                   dsmoe_stream_t stream);
 
+/* dsmoe_forward for T <= 8 without a context and without allocating: no
+ * counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The scratch between the launches is a static 16 MiB
+ * device array per GPU, set up when the library loads its kernels on that
+ * device (dsmoe_init or the first call); a layer whose scratch for 8 tokens
+ * exceeds it (or T > 8) is rejected with DSMOE_ERR_UNSUPPORTED.  Same
+ * arguments and results as dsmoe_forward.  All calls on one GPU share the
+ * array: calls that overlap on one GPU (two streams, two threads) race. */
+int dsmoe_forward_noalloc(const dsmoe_config* cfg, const dsmoe_weights* w, const float* x, int32_t T,
+                          float* shared_out, float* routed_out, int32_t* selected, float* weights,
+                          dsmoe_stream_t stream);
+
 /* Per-stage timing of dsmoe_forward (no reference counterpart: the
  * reference has no tracing).  When enabled, every stage of the forward is
  * bracketed by hipEvents on the caller's stream; dsmoe_profile_read waits
