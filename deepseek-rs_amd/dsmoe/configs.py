@@ -12,6 +12,9 @@ C4        : C2 with T=128 (N(0,0.02) router); C4-tie: identical router rows,
 C5        : C2 with T=2048 and a Zipf(1.1) popularity prior over a seeded
             expert permutation.  The layer's logits are x.W, so the prior
             enters through the selection bias (-1.1 ln rank).
+REF       : the reference's own layer (engine/src/model.rs:4,15-18,
+            session.rs:21): d=4096, E=256, top-6, no groups, scale 1.5, no
+            correction bias, I=2048, Q8_0 shared expert I_s=2048.
 
 Weights are N(0, 0.02) quantized by this library's encoders; router weights
 N(0, 0.02) in f16; the correction bias N(0, 0.01).
@@ -52,6 +55,9 @@ CASES = {
     "c4": Case("c4", C2_CFG, T=128, d_ff_real=2048, d_ff_shared_real=2048),
     "c4tie": Case("c4tie", C2_CFG, T=128, d_ff_real=2048, d_ff_shared_real=2048, router_tie=True),
     "c5": Case("c5", C2_CFG, T=2048, d_ff_real=2048, d_ff_shared_real=2048, zipf=1.1),
+    "ref": Case("ref", MoeConfig(d_model=4096, d_ff=2048, n_expert=256, top_k=6, n_group=1, topk_group=1,
+                                 route_scale=1.5, swiglu_clamp=10.0, has_bias=False, shared_fmt=0,
+                                 d_ff_shared=2048), T=1, d_ff_real=2048, d_ff_shared_real=2048),
 }
 
 

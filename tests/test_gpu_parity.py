@@ -394,6 +394,8 @@ def _host_weights(w):
 
 
 def _run_layer(case, T, gpu, sample=None):
+    """`sample`: rows checked against the oracle (None = all), or a function
+    of the GPU's routing [T][k] that picks them."""
     import torch
     say(f"layer {case.name} T={T}")
     w = C.make_weights(case, device=gpu)
@@ -407,7 +409,8 @@ def _run_layer(case, T, gpu, sample=None):
     layer.forward(w, x, so, ro, sel, wt)
     torch.cuda.synchronize()
     hw = _host_weights(w)
-    rows = np.arange(T) if sample is None else sample
+    rows = np.arange(T) if sample is None else sample(np_(sel)) if callable(sample) else sample
+    say(f"  oracle rows: {len(rows)}")
     xs = np_(x)[rows].copy()
     so0, ro0, sel0, wt0 = O.moe_forward(case.cfg, hw, xs, len(rows), NT)
     assert np.array_equal(np_(sel)[rows], sel0), "routing differs"
@@ -447,9 +450,43 @@ def test_layer_c4_tie_routing(gpu):
     assert (sel == sel[0]).all()
 
 
+def test_layer_c4_binomial(gpu):
+    """128 tokens with N(0, 0.02) routers, so expert loads
+    are roughly Binomial(128, 8/256); every second row against the oracle."""
+    sel, _, _ = _run_layer(C.CASES["c4"], 128, gpu, sample=np.arange(0, 128, 2))
+    counts = np.bincount(sel.reshape(-1), minlength=256)
+    say(f"  c4 expert loads: max {counts.max()}, experts used {np.count_nonzero(counts)}")
+    assert np.count_nonzero(counts) > 64
+
+
+@pytest.mark.parametrize("T", [1, 128])
+def test_layer_reference_config(gpu, T):
+    """The reference's own layer shape and routing (d=4096, E=256, top-6, no
+    groups, scale 1.5, no bias) at decode and at a 128-token batch."""
+    _run_layer(C.with_tokens(C.CASES["ref"], T), T, gpu)
+
+
+def _hot_and_cold_rows(sel, n=256, seed=5):
+    """Rows holding the 16 coldest used experts and the hottest expert,
+    topped up with random rows to n."""
+    T = sel.shape[0]
+    counts = np.bincount(sel.reshape(-1), minlength=256)
+    used = np.flatnonzero(counts)
+    cold = used[np.argsort(counts[used], kind="stable")[:16]]
+    hot = int(np.argmax(counts))
+    rows = set(np.flatnonzero(np.isin(sel, cold).any(1)).tolist())
+    rows |= set(np.flatnonzero((sel == hot).any(1))[:64].tolist())
+    rest = np.random.default_rng(seed).permutation(T)
+    for r in rest:
+        if len(rows) >= n:
+            break
+        rows.add(int(r))
+    return np.array(sorted(rows))
+
+
 def test_layer_c5_zipf_sampled(gpu):
     case = C.CASES["c5"]
-    sel, _, _ = _run_layer(case, 2048, gpu, sample=np.arange(0, 2048, 97))
+    sel, _, _ = _run_layer(case, 2048, gpu, sample=_hot_and_cold_rows)
     counts = np.bincount(sel.reshape(-1), minlength=256)
     top10 = np.sort(counts)[::-1][:10].sum() / counts.sum()
     say(f"  top-10 expert share at T=2048 Zipf: {top10:.3f}")
@@ -480,4 +517,38 @@ def test_decode_calls_in_a_row(gpu, name, Ts):
         assert np.array_equal(np_(sel), sel0)
         assert bits_equal(np_(wt), wt0)
         assert bits_equal(np_(ro), ro0) and bits_equal(np_(so), so0), f"call {rep} differs from the oracle"
+    lay.close()
+
+
+@pytest.mark.parametrize("name", ["ref", "c2"])
+def test_token_by_token_equals_one_batch(gpu, name):
+    """128 calls with T = 1 (the matvec launches) against one call with
+    T = 128 (the grouped GEMMs) on the same context: the same routing bits
+    and the same outputs, so a caller may split a prefill into chunks of any
+    size (session.rs:795-895 runs the layer once per chunk)."""
+    import torch
+    case = C.with_tokens(C.CASES[name], 128)
+    T, d, k = 128, case.cfg.d_model, case.cfg.top_k
+    say(f"token by token vs batch {name} T={T}")
+    w = C.make_weights(case, device=gpu)
+    x = C.make_x(case, T=T, device=gpu)
+    lay = dsmoe.MoeLayer(case.cfg, T)
+    outs = []
+    for mode in ("batch", "tokens"):
+        so = torch.full((T, d), float("nan"), device=gpu)
+        ro = torch.full((T, d), float("nan"), device=gpu)
+        sel = torch.full((T, k), -7, dtype=torch.int32, device=gpu)
+        wt = torch.full((T, k), float("nan"), device=gpu)
+        if mode == "batch":
+            lay.forward(w, x, so, ro, sel, wt)
+        else:
+            for t in range(T):
+                lay.forward(w, x[t:t + 1], so[t:t + 1], ro[t:t + 1], sel[t:t + 1], wt[t:t + 1])
+        torch.cuda.synchronize()
+        outs.append([np_(v) for v in (so, ro, sel, wt)])
+    (sb, rb, selb, wb), (st, rt, selt, wtt) = outs
+    assert np.array_equal(selb, selt) and bits_equal(wb, wtt)
+    e1 = assert_close(rt, rb, f"{name} routed_out tokens vs batch")
+    e2 = assert_close(st, sb, f"{name} shared_out tokens vs batch")
+    assert e1 == 1.0 and e2 == 1.0, "chunked and batched outputs differ in bits"
     lay.close()
