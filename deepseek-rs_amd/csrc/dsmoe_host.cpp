@@ -84,15 +84,15 @@ const std::vector<uint8_t>& lvlmap_host() {
 enum Kern { K_PREP, K_ROUTER_SELECT, K_UP, K_MIDQ, K_DN, K_SWIGLU, K_MOE_SUM, K_DISPATCH, K_SYNTH,
             K_GU_GROUPED, K_DN_GROUPED, K_Q80_GEMM_SWIGLU, K_Q80_GEMM,
             K_ROUTER_TILE, K_UP_ROWS, K_DN_ROWS, K_Q80_GEMM_SWIGLU_J7, K_Q80_GEMM_J7, K_Q80_GEMM_SWIGLU_J2,
-            K_Q80_GEMM_J2, K_COUNT };
+            K_Q80_GEMM_J2, K_HC_EXPAND, K_COUNT };
 const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_up", "dsmoe_midq", "dsmoe_dn",
                                    "dsmoe_swiglu", "dsmoe_moe_sum", "dsmoe_dispatch", "dsmoe_synth",
                                    "dsmoe_gu_grouped", "dsmoe_dn_grouped", "dsmoe_q80_gemm_swiglu", "dsmoe_q80_gemm",
                                    "dsmoe_router_tile",
                                    "dsmoe_up_rows", "dsmoe_dn_rows", "dsmoe_q80_gemm_swiglu_j7", "dsmoe_q80_gemm_j7",
-                                   "dsmoe_q80_gemm_swiglu_j2", "dsmoe_q80_gemm_j2"};
+                                   "dsmoe_q80_gemm_swiglu_j2", "dsmoe_q80_gemm_j2", "dsmoe_hc_expand"};
 // code object of each kernel: 0 = dsmoe_kernels.hsaco, 1 = dsmoe_gemm.hsaco (same directory)
-const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1};
+const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0};
 static_assert(DSMOE_GROUPED_TILE_M == kGuBM, "header and kernels disagree on the grouped tile");
 
 extern "C" int dsmoe_noalloc_setup(void** ptr, size_t* bytes);  // dsmoe_noalloc.hip
@@ -488,6 +488,21 @@ int dsmoe_q8_0_matvec(const void* w, const int8_t* xq, const float* xscale, floa
   }
   a.sh_tiles = sh.tiles;
   return launch(K_DN, dim3(a.sh_tiles * a.sh_work), dim3(sh.block), q80_lds(in_dim / 32, 1, sh.R), stream, a);
+}
+
+int dsmoe_hc_expand(const float* block_out, const float* block_add, const float* residual_hc, const float* split,
+                    float* out_hc, int32_t n_embd, int32_t n_hc, int32_t n_tokens, int32_t mix_hc, int32_t has_add,
+                    dsmoe_stream_t stream) {
+  if (!block_out || !residual_hc || !split || !out_hc || (has_add && !block_add))
+    return fail(DSMOE_ERR_INVALID, "hc_expand: null pointer");
+  if (n_embd < 0 || n_hc < 1 || n_tokens < 0 || mix_hc < 2 * n_hc + n_hc * n_hc)
+    return fail(DSMOE_ERR_INVALID, "hc_expand: bad shape (mix_hc must hold pre, post and comb)");
+  HcExpandArgs a{block_out, has_add ? block_add : nullptr, residual_hc, split, out_hc, n_embd, n_hc, n_tokens, mix_hc,
+                 has_add ? 1 : 0};
+  const size_t n = (size_t)n_tokens * n_hc * n_embd;
+  const size_t threads = hc_expand_vec_ok(a) ? n / 4 : n;
+  if ((threads + 255) / 256 > 0x7FFFFFFF) return fail(DSMOE_ERR_UNSUPPORTED, "hc_expand: too large");
+  return launch(K_HC_EXPAND, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, a);
 }
 
 int dsmoe_swiglu(const float* gate, const float* up, float* out, int32_t n, float clamp, float weight,

@@ -216,6 +216,23 @@ inline __host__ __device__ bool moe_sum_vec_ok(const MoeSumArgs& a) {
   return a.d % 4 == 0 && (((uintptr_t)a.down | (uintptr_t)a.out) & 15) == 0;
 }
 
+// FFN residual merge (hc.rs:212-259): out[t][dst][i] from the layer output,
+// the residual streams and the token's split row.
+struct HcExpandArgs {
+  const float* block_out;    // [T][n_embd]
+  const float* block_add;    // [T][n_embd] (read when has_add)
+  const float* residual_hc;  // [T][n_hc][n_embd]
+  const float* split;        // [T][mix_hc]: pre[n_hc] | post[n_hc] | comb[n_hc][n_hc]
+  float* out_hc;             // [T][n_hc][n_embd]
+  int32_t n_embd, n_hc, T, mix_hc, has_add;
+};
+// Four outputs per thread with 16-byte accesses.
+inline __host__ __device__ bool hc_expand_vec_ok(const HcExpandArgs& a) {
+  return a.n_embd % 4 == 0 &&
+         (((uintptr_t)a.block_out | (uintptr_t)a.residual_hc | (uintptr_t)a.out_hc |
+           (a.has_add ? (uintptr_t)a.block_add : 0)) & 15) == 0;
+}
+
 struct DispatchArgs {
   const int32_t* selected;  // [pairs]
   uint32_t* counts;         // [E]

@@ -1814,6 +1814,44 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_moe_sum(const MoeSumArgs
   a.out[i] = acc;
 }
 
+// hc.rs:212-259.  One thread per output element, or per four consecutive
+// elements of one (token, destination stream) with 16-byte accesses; the
+// split row is the same for a whole (token, destination) and comes from cache.
+// Sums in the reference's order: (out (+ add)) * post, then + comb * residual
+// for src = 0, 1, ... (no fused multiply-add).
+extern "C" __global__ __launch_bounds__(256) void dsmoe_hc_expand(const HcExpandArgs a) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t per_tok = (size_t)a.n_hc * a.n_embd;
+  const bool vec = hc_expand_vec_ok(a);
+  const size_t e0 = vec ? 4 * i : i;
+  if (e0 >= (size_t)a.T * per_tok) return;
+  const size_t t = e0 / per_tok, rem = e0 % per_tok;
+  const int dst = (int)(rem / a.n_embd), col = (int)(rem % a.n_embd);
+  const float* row = a.split + t * a.mix_hc;
+  const float post = row[a.n_hc + dst];
+  const float* res = a.residual_hc + t * per_tok + col;
+  if (vec) {
+    float4 v = *(const float4*)(a.block_out + t * a.n_embd + col);
+    if (a.has_add) {
+      const float4 b = *(const float4*)(a.block_add + t * a.n_embd + col);
+      v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
+    }
+    float4 acc = make_float4(v.x * post, v.y * post, v.z * post, v.w * post);
+    for (int src = 0; src < a.n_hc; src++) {
+      const float c = row[2 * a.n_hc + dst + src * a.n_hc];
+      const float4 r = *(const float4*)(res + (size_t)src * a.n_embd);
+      acc.x = acc.x + c * r.x; acc.y = acc.y + c * r.y; acc.z = acc.z + c * r.z; acc.w = acc.w + c * r.w;
+    }
+    *(float4*)(a.out_hc + e0) = acc;
+    return;
+  }
+  float v = a.block_out[t * a.n_embd + col];
+  if (a.has_add) v = v + a.block_add[t * a.n_embd + col];
+  float acc = v * post;
+  for (int src = 0; src < a.n_hc; src++) acc = acc + row[2 * a.n_hc + dst + src * a.n_hc] * res[(size_t)src * a.n_embd];
+  a.out_hc[e0] = acc;
+}
+
 // ---------------------------------------------------------------------------
 // Dispatch (moe.rs:299-362, :547-596) as one 1024-thread workgroup: per-wave
 // expert histograms, an exclusive scan over (expert, wave), then a stable

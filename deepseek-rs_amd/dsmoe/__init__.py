@@ -25,7 +25,7 @@ IQ2XXS_BYTES, Q2K_BYTES, Q8K_BYTES, Q8_0_BYTES = 66, 84, 292, 34
 
 EXPORTED = [
     "dsmoe_version", "dsmoe_last_error", "dsmoe_init", "dsmoe_create", "dsmoe_destroy",
-    "dsmoe_scratch_bytes", "dsmoe_forward", "dsmoe_forward_noalloc", "dsmoe_router_logits", "dsmoe_router_select",
+    "dsmoe_scratch_bytes", "dsmoe_forward", "dsmoe_forward_noalloc", "dsmoe_hc_expand", "dsmoe_router_logits", "dsmoe_router_select",
     "dsmoe_q8k_quantize", "dsmoe_q8_0_quantize", "dsmoe_gate_up_mid", "dsmoe_down", "dsmoe_moe_sum",
     "dsmoe_q8_0_matvec", "dsmoe_swiglu", "dsmoe_dispatch", "dsmoe_tensor_bytes", "dsmoe_synth_tensor",
     "dsmoe_synth_tensor_host", "dsmoe_stage_name", "dsmoe_set_profiling", "dsmoe_profile_read",
@@ -74,6 +74,7 @@ def lib():
         "dsmoe_destroy": ([vp], i32),
         "dsmoe_scratch_bytes": ([vp], ctypes.c_size_t),
         "dsmoe_forward": ([vp, ctypes.POINTER(Weights), vp, i32, vp, vp, vp, vp, vp], i32),
+        "dsmoe_hc_expand": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp], i32),
         "dsmoe_forward_noalloc": ([ctypes.POINTER(Config), ctypes.POINTER(Weights), vp, i32, vp, vp, vp, vp, vp], i32),
         "dsmoe_router_logits": ([vp, vp, vp, i32, i32, i32, vp], i32),
         "dsmoe_router_select": ([ctypes.POINTER(Config), vp, vp, i32, vp, vp, vp, vp], i32),
@@ -292,6 +293,12 @@ class LayerWeights:
     def c(self) -> Weights:
         return Weights(*[(_p(getattr(self, n)).value or None) for n in
                          ("router_f16", "bias", "gate", "up", "down", "sh_gate", "sh_up", "sh_down")])
+
+
+def hc_expand(block_out, block_add, residual_hc, split, out_hc, n_embd, n_hc, T, mix_hc, has_add, stream=None):
+    """hc_expand (hc.rs:212-259): the residual merge after the layer."""
+    check(lib().dsmoe_hc_expand(_p(block_out), _p(block_add), _p(residual_hc), _p(split), _p(out_hc), n_embd, n_hc, T,
+                                mix_hc, int(has_add), _stream(stream)))
 
 
 def forward_noalloc(cfg, w, x, shared_out, routed_out, selected=None, weights=None, stream=None):

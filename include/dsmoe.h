@@ -219,6 +219,17 @@ int dsmoe_down(const void* down, const void* midq, const int32_t* selected, floa
 /* moe_sum (engine/src/kernels/moe.rs:983-1005). */
 int dsmoe_moe_sum(const float* down, float* out, int32_t d, int32_t k, int32_t T, dsmoe_stream_t stream);
 
+/* hc_expand (engine/src/kernels/hc.rs:212-259), the FFN residual merge that
+ * consumes the layer's outputs (session.rs:2157-2175: block_out =
+ * shared_out, block_add = routed_out, has_add = 1 after a MoE layer):
+ *   out_hc[t][dst][i] = (block_out[t][i] (+ block_add[t][i])) * post[dst]
+ *                       + sum_src comb[dst + src*n_hc] * residual_hc[t][src][i]
+ * with post = split[t*mix_hc + n_hc ..] and comb = split[t*mix_hc + 2*n_hc ..].
+ * block_add may be NULL when has_add = 0. */
+int dsmoe_hc_expand(const float* block_out, const float* block_add, const float* residual_hc, const float* split,
+                    float* out_hc, int32_t n_embd, int32_t n_hc, int32_t n_tokens, int32_t mix_hc, int32_t has_add,
+                    dsmoe_stream_t stream);
+
 /* matmul_q8_0_preq_warp8 / _batch_warp8 (engine/src/kernels/matmul.rs:357-458).
  * in_dim a multiple of 64. */
 int dsmoe_q8_0_matvec(const void* w, const int8_t* xq, const float* xscale, float* out, int32_t in_dim,

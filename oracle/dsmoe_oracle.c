@@ -27,8 +27,12 @@
  *   grouped routing (n_group > 1)  brute force over all group subsets (no reference
  *                                  counterpart: the reference has no group-limited top-k)
  *   or_dispatch                    numpy stable argsort; prefix sums
- *   or_moe_forward                 float64 dequantise-then-GEMM closed form within the
- *                                  Q8_K quantisation error
+ *   or_moe_sum                     f32 values whose sum depends on the slot order
+ *   or_hc_expand                   dyadic inputs (exact in f32) vs the float64 formula, with
+ *                                  a non-symmetric comb; numpy f32 in the reference's order
+ *   or_moe_forward                 float64 dequantise-then-GEMM closed form through the same
+ *                                  activation quantizers, within 1e-3, with the SwiGLU clamp
+ *                                  active on ~18 % of the products
  */
 #include "dsmoe_oracle.h"
 
@@ -531,6 +535,26 @@ void or_moe_sum(const float* down, float* out, int d, int k, int T) {
       for (int s = 0; s < k; s++) acc += down[((size_t)t * k + s) * d + r];
       out[(size_t)t * d + r] = acc;
     }
+}
+
+/* hc_expand (engine/src/kernels/hc.rs:212-259): the FFN residual merge
+ * after the layer (session.rs:2157-2175).  out[t][dst][i] =
+ * (block_out + block_add)[t][i] * post[dst] + sum over src in order of
+ * comb[dst + src*n_hc] * residual[t][src][i], where post and comb are the
+ * token's split row at offsets n_hc and 2*n_hc.  f32, no fused multiply-add. */
+void or_hc_expand(const float* block_out, const float* block_add, const float* residual_hc, const float* split,
+                  float* out_hc, int n_embd, int n_hc, int n_tokens, int mix_hc, int has_add) {
+  for (int t = 0; t < n_tokens; t++)
+    for (int dst = 0; dst < n_hc; dst++)
+      for (int i = 0; i < n_embd; i++) {
+        float v = block_out[(size_t)t * n_embd + i];
+        if (has_add) v += block_add[(size_t)t * n_embd + i];
+        const float* row = split + (size_t)t * mix_hc;
+        float acc = v * row[n_hc + dst];
+        for (int src = 0; src < n_hc; src++)
+          acc += row[2 * n_hc + dst + src * n_hc] * residual_hc[((size_t)t * n_hc + src) * n_embd + i];
+        out_hc[((size_t)t * n_hc + dst) * n_embd + i] = acc;
+      }
 }
 
 /* ------------------------------------------------------------------ */

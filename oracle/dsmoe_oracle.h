@@ -68,6 +68,8 @@ void or_gate_up_mid(const uint8_t* gate, const uint8_t* up, const uint8_t* xq,
 void or_down(const uint8_t* down, const uint8_t* midq, const int32_t* selected,
              float* down_out, int d, int I, int T, int k, int nthreads);
 void or_moe_sum(const float* down, float* out, int d, int k, int T);
+void or_hc_expand(const float* block_out, const float* block_add, const float* residual_hc, const float* split,
+                  float* out_hc, int n_embd, int n_hc, int n_tokens, int mix_hc, int has_add);
 
 /* dispatch */
 void or_dispatch(const int32_t* selected, int pairs, int E, int block_m,

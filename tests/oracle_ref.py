@@ -61,6 +61,7 @@ def load():
         "or_gate_up_mid": ([vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, i32], None),
         "or_down": ([vp, vp, vp, vp, i32, i32, i32, i32, i32], None),
         "or_moe_sum": ([vp, vp, i32, i32, i32], None),
+        "or_hc_expand": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, i32], None),
         "or_dispatch": ([vp, i32, i32, i32, vp, vp, vp, vp, vp, vp], None),
         "or_moe_forward": ([ctypes.POINTER(OrConfig), vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, vp, vp, vp, i32], i32),
     }
@@ -116,6 +117,14 @@ def dispatch(sel, E, block_m):
     load().or_dispatch(P(np.ascontiguousarray(sel, np.int32)), pairs, E, block_m, P(counts), P(offsets), P(sp),
                        P(to), P(te), P(ts))
     return counts, offsets, sp[:pairs], to, te[:to[E]], ts[:to[E]]
+
+
+def hc_expand(block_out, block_add, residual_hc, split, n_embd, n_hc, T, mix_hc, has_add):
+    out = np.zeros(T * n_hc * n_embd, np.float32)
+    f = lambda a: None if a is None else np.ascontiguousarray(a, np.float32)
+    load().or_hc_expand(P(f(block_out)), P(f(block_add)), P(f(residual_hc)), P(f(split)), P(out), n_embd, n_hc, T,
+                        mix_hc, int(has_add))
+    return out.reshape(T, n_hc, n_embd)
 
 
 def moe_forward(mcfg, w, x, T, nthreads=8):

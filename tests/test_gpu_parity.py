@@ -552,3 +552,31 @@ def test_token_by_token_equals_one_batch(gpu, name):
     e2 = assert_close(st, sb, f"{name} shared_out tokens vs batch")
     assert e1 == 1.0 and e2 == 1.0, "chunked and batched outputs differ in bits"
     lay.close()
+
+
+@pytest.mark.parametrize("n,n_hc,T,has_add,mix,offset", [(4096, 4, 1, 1, 24, 0), (4096, 4, 5, 0, 24, 0),
+                                                          (1000, 3, 2, 1, 15, 0), (4096, 4, 3, 1, 24, 1),
+                                                          (7168, 2, 9, 1, 8, 0)])
+def test_hc_expand_bitexact(gpu, n, n_hc, T, has_add, mix, offset):
+    """hc_expand against the oracle, bit for bit: the vector form (n % 4 == 0,
+    16-byte aligned), the scalar form (n = 1000, or buffers one float off
+    16-byte alignment), has_add 0 and 1."""
+    import torch
+    say(f"hc_expand n={n} n_hc={n_hc} T={T} has_add={has_add} mix={mix} offset={offset}")
+    rng = np.random.default_rng(n + T)
+    bo = rng.normal(0, 1, (T, n)).astype(np.float32)
+    ba = rng.normal(0, 1, (T, n)).astype(np.float32)
+    res = rng.normal(0, 1, (T, n_hc, n)).astype(np.float32)
+    split = rng.normal(0, 1, (T, mix)).astype(np.float32)
+
+    def dev(a):  # a device copy starting `offset` floats into its allocation
+        buf = torch.empty(a.size + offset, dtype=torch.float32, device=gpu)
+        v = buf[offset:]
+        v.copy_(torch.from_numpy(a.reshape(-1)))
+        return v
+
+    out = torch.full((T * n_hc * n + offset,), float("nan"), device=gpu)[offset:]
+    dsmoe.hc_expand(dev(bo), dev(ba) if has_add else None, dev(res), dev(split), out, n, n_hc, T, mix, has_add)
+    torch.cuda.synchronize()
+    want = O.hc_expand(bo, ba if has_add else None, res, split, n, n_hc, T, mix, has_add)
+    assert bits_equal(np_(out).reshape(T, n_hc, n), want)

@@ -498,3 +498,57 @@ def test_moe_sum_is_slot_ordered(oracle):
             want[t] = (want[t] + down[t, j]).astype(np.float32)
     assert np.array_equal(out.reshape(T, d).view(np.uint32), want.view(np.uint32))
     assert out[0] == 0.0 and out[2] == 1.0
+
+
+# ---------------------------------------------------------------- hc_expand
+def _hc_inputs(rng, T, n_hc, n, mix, dyadic):
+    if dyadic:  # multiples of 1/8 in [-4, 4]: every product and sum below is exact in f32
+        g = lambda *s: (rng.integers(-32, 33, s) / 8.0).astype(np.float32)
+    else:
+        g = lambda *s: rng.normal(0, 1, s).astype(np.float32)
+    return g(T, n), g(T, n), g(T, n_hc, n), g(T, mix)
+
+
+@pytest.mark.parametrize("n_hc,has_add", [(4, 1), (4, 0), (3, 1), (1, 1)])
+def test_hc_expand_closed_form(oracle, n_hc, has_add):
+    """Exact in f32 on dyadic inputs, so the oracle must equal the float64
+    formula of hc.rs:212-259 bit for bit; comb is not symmetric, so a
+    transposed comb index (src + dst*n_hc) fails, as does a post/comb offset
+    off by n_hc or a dropped block_add."""
+    rng = np.random.default_rng(40 + n_hc)
+    T, n = 3, 40
+    mix = 2 * n_hc + n_hc * n_hc + 2  # the reference's row stride may exceed the split
+    bo, ba, res, split = _hc_inputs(rng, T, n_hc, n, mix, True)
+    got = oracle_ref.hc_expand(bo, ba, res, split, n, n_hc, T, mix, has_add)
+    want = np.zeros((T, n_hc, n))
+    for t in range(T):
+        v = bo[t].astype(np.float64) + (ba[t] if has_add else 0)
+        post = split[t, n_hc:2 * n_hc].astype(np.float64)
+        comb = split[t, 2 * n_hc:2 * n_hc + n_hc * n_hc].astype(np.float64).reshape(n_hc, n_hc)  # [src][dst]
+        for dst in range(n_hc):
+            want[t, dst] = v * post[dst] + comb[:, dst] @ res[t].astype(np.float64)
+    assert np.array_equal(got.astype(np.float64), want)
+    if n_hc > 1:
+        assert not np.allclose(comb, comb.T)
+
+
+def test_hc_expand_float64_and_order(oracle):
+    """Random normal inputs: within f32 rounding of the float64 formula, and
+    bit-equal to a numpy f32 evaluation in the reference's order."""
+    rng = np.random.default_rng(9)
+    T, n_hc, n, mix = 2, 4, 4096, 24
+    bo, ba, res, split = _hc_inputs(rng, T, n_hc, n, mix, False)
+    got = oracle_ref.hc_expand(bo, ba, res, split, n, n_hc, T, mix, 1)
+    f = np.float32
+    want = np.zeros((T, n_hc, n), np.float32)
+    for t in range(T):
+        v = (bo[t] + ba[t]).astype(f)
+        for dst in range(n_hc):
+            acc = (v * split[t, n_hc + dst]).astype(f)
+            for src in range(n_hc):
+                acc = (acc + (split[t, 2 * n_hc + dst + src * n_hc] * res[t, src]).astype(f)).astype(f)
+            want[t, dst] = acc
+            w64 = (bo[t].astype(np.float64) + ba[t]) * split[t, n_hc + dst] + sum(
+                float(split[t, 2 * n_hc + dst + s * n_hc]) * res[t, s].astype(np.float64) for s in range(n_hc))
+            assert np.max(np.abs(got[t, dst] - w64)) < 1e-5 * (1 + np.max(np.abs(w64)))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
