@@ -979,3 +979,37 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_router_tile(const Router
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Peak probes (no reference counterpart): the bench reports the sustained
+// MFMA rate and HBM read rate of the box next to the published peaks.
+// ---------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(256) void dsmoe_probe_mfma(const ProbeArgs a) {
+  const int lane = threadIdx.x & 63;
+  half8 x, y;
+  for (int j = 0; j < 8; j++) {
+    x[j] = (_Float16)(0.001f * (float)((lane + j) & 7));
+    y[j] = (_Float16)(0.002f * (float)((lane * 3 + j) & 7));
+  }
+  float16v acc[8];
+  for (int c = 0; c < 8; c++)
+    for (int j = 0; j < 16; j++) acc[c][j] = 0.0f;
+  for (int64_t it = 0; it < a.iters; it++) {
+#pragma unroll
+    for (int c = 0; c < 8; c++) acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x, y, acc[c], 0, 0, 0);
+  }
+  float s = 0.0f;
+  for (int c = 0; c < 8; c++)
+    for (int j = 0; j < 16; j++) s = s + acc[c][j];
+  if (s == 1234.5f) a.sink[blockIdx.x] = s;  // never true; keeps the chain live
+}
+
+extern "C" __global__ __launch_bounds__(256) void dsmoe_probe_read(const ProbeArgs a) {
+  uint32_t x = 0;
+#pragma unroll 8
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n16; i += (uint64_t)gridDim.x * blockDim.x) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)a.src + i);
+    x ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (x == 0x9E3779B9u) a.sink[blockIdx.x] = (float)x;  // data-dependent, almost never taken
+}

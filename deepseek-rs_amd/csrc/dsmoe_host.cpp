@@ -84,15 +84,16 @@ const std::vector<uint8_t>& lvlmap_host() {
 enum Kern { K_PREP, K_ROUTER_SELECT, K_UP, K_MIDQ, K_DN, K_SWIGLU, K_MOE_SUM, K_DISPATCH, K_SYNTH,
             K_GU_GROUPED, K_DN_GROUPED, K_Q80_GEMM_SWIGLU, K_Q80_GEMM,
             K_ROUTER_TILE, K_UP_ROWS, K_DN_ROWS, K_Q80_GEMM_SWIGLU_J7, K_Q80_GEMM_J7, K_Q80_GEMM_SWIGLU_J2,
-            K_Q80_GEMM_J2, K_HC_EXPAND, K_COUNT };
+            K_Q80_GEMM_J2, K_HC_EXPAND, K_PROBE_MFMA, K_PROBE_READ, K_UP_EM, K_DN_EM, K_COUNT };
 const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_up", "dsmoe_midq", "dsmoe_dn",
                                    "dsmoe_swiglu", "dsmoe_moe_sum", "dsmoe_dispatch", "dsmoe_synth",
                                    "dsmoe_gu_grouped", "dsmoe_dn_grouped", "dsmoe_q80_gemm_swiglu", "dsmoe_q80_gemm",
                                    "dsmoe_router_tile",
                                    "dsmoe_up_rows", "dsmoe_dn_rows", "dsmoe_q80_gemm_swiglu_j7", "dsmoe_q80_gemm_j7",
-                                   "dsmoe_q80_gemm_swiglu_j2", "dsmoe_q80_gemm_j2", "dsmoe_hc_expand"};
+                                   "dsmoe_q80_gemm_swiglu_j2", "dsmoe_q80_gemm_j2", "dsmoe_hc_expand",
+                                   "dsmoe_probe_mfma", "dsmoe_probe_read", "dsmoe_up_em", "dsmoe_dn_em"};
 // code object of each kernel: 0 = dsmoe_kernels.hsaco, 1 = dsmoe_gemm.hsaco (same directory)
-const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0};
+const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0, 1, 1, 0, 0};
 static_assert(DSMOE_GROUPED_TILE_M == kGuBM, "header and kernels disagree on the grouped tile");
 
 extern "C" int dsmoe_noalloc_setup(void** ptr, size_t* bytes);  // dsmoe_noalloc.hip
@@ -177,7 +178,8 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // the workgroup (<= 1024 threads) and the grid has at least ~2 workgroups
 // per CU (256 CUs).
 constexpr int kMinWgs = 512;
-constexpr int kDecodeMaxT = kMaxDecodeT;  // row-streaming (matvec) launches up to 8 tokens, grouped GEMMs above
+constexpr int kDecodeMaxT = kMaxDecodeT;
+constexpr int kEmMaxLoad = 4;  // pairs per expert (on average) up to which batches run expert-major  // row-streaming (matvec) launches up to 8 tokens, grouped GEMMs above
 
 int pow2_floor(int v) {
   int p = 1;
@@ -222,6 +224,14 @@ int select_wave_p(const dsmoe_config& cf) {
     return (lpg == 1 || lpg == 2 || lpg == 4 || lpg == 8 || lpg == 16) ? P : 0;
   }
   return 0;
+}
+// Expert-major launches (dsmoe_up_em / dsmoe_dn_em): shapes they take.  The
+// gate/up workgroup stages kEmPairs activations in at most 61 KB of LDS.
+size_t gate_up_em_lds(int nb) { return 3072 + (size_t)kEmPairs * nb * 272; }
+size_t down_em_lds(int nb) { return (size_t)((kEmPairs * nb + 3) / 4 * 4) * 4 + (size_t)kEmPairs * nb * (32 + 272); }
+bool em_fits(const dsmoe_config& cf) {
+  return up_rows_fits(cf.d_model) && gate_up_em_lds(cf.d_model / 256) <= 64 * 1024 && cf.d_ff <= 2048 &&
+         cf.d_ff % 256 == 0;
 }
 int q80_rows_tiles(int out_dim, bool two) { return two ? (out_dim + 3) / 4 : (out_dim + 7) / 8; }
 size_t gate_up_lds(int nb, int R) { return 3072 + (size_t)align_up(nb, 4) * 4 + (size_t)nb * 272 + (size_t)2 * R * nb * 4; }
@@ -490,6 +500,24 @@ int dsmoe_q8_0_matvec(const void* w, const int8_t* xq, const float* xscale, floa
   return launch(K_DN, dim3(a.sh_tiles * a.sh_work), dim3(sh.block), q80_lds(in_dim / 32, 1, sh.R), stream, a);
 }
 
+int dsmoe_probe(int32_t kind, const void* src, size_t bytes, int64_t iters, float* sink, dsmoe_stream_t stream) {
+  if (!sink) return fail(DSMOE_ERR_INVALID, "probe: sink is NULL");
+  int dev = 0, cus = 0;
+  DSM_CHECK_HIP(hipGetDevice(&dev));
+  DSM_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  if (kind == 0) {
+    if (iters < 1) return fail(DSMOE_ERR_INVALID, "probe: iters < 1");
+    ProbeArgs a{nullptr, sink, 0, iters};
+    return launch(K_PROBE_MFMA, dim3(2u * cus), dim3(256), 0, stream, a);  // two waves per SIMD
+  }
+  if (kind == 1) {
+    if (!src || bytes < 16 || ((uintptr_t)src & 15)) return fail(DSMOE_ERR_INVALID, "probe: bad source buffer");
+    ProbeArgs a{(const uint4*)src, sink, bytes / 16, 0};
+    return launch(K_PROBE_READ, dim3(8u * cus), dim3(256), 0, stream, a);
+  }
+  return fail(DSMOE_ERR_INVALID, "probe: unknown kind");
+}
+
 int dsmoe_hc_expand(const float* block_out, const float* block_add, const float* residual_hc, const float* split,
                     float* out_hc, int32_t n_embd, int32_t n_hc, int32_t n_tokens, int32_t mix_hc, int32_t has_add,
                     dsmoe_stream_t stream) {
@@ -562,6 +590,54 @@ int dsmoe_down_sorted(const void* down, const uint16_t* mh, const void* mq, cons
                   tile_starts, down_out, d, I, E};
   const int max_tiles = pairs / kGuBM + std::min(E, pairs);
   return launch(K_DN_GROUPED, dim3(xcd_grid(max_tiles, d / kDnBN)), dim3(256), 0, stream, a);
+}
+
+int dsmoe_gate_up_mid_em(const void* gate, const void* up, const void* xq, const uint32_t* sorted_pairs,
+                         const uint32_t* offsets, const uint32_t* tile_offsets, const uint32_t* tile_experts,
+                         const uint32_t* tile_starts, const float* weights, float* mid_out, int32_t d, int32_t I,
+                         int32_t k, int32_t E, int32_t pairs, float clamp, dsmoe_stream_t stream) {
+  if (!gate || !up || !xq || !sorted_pairs || !offsets || !tile_offsets || !tile_experts || !tile_starts || !mid_out)
+    return fail(DSMOE_ERR_INVALID, "gate_up_mid_em: null pointer");
+  if (!aligned16(gate) || !aligned16(up)) return fail(DSMOE_ERR_INVALID, "gate_up_mid_em: weights must be 16-byte aligned");
+  if (!up_rows_fits(d) || gate_up_em_lds(d / 256) > 64 * 1024)
+    return fail(DSMOE_ERR_UNSUPPORTED, "gate_up_mid_em: d must be a multiple of 512, at most 7168");
+  if (I <= 0 || k <= 0 || E <= 0 || pairs < 0) return fail(DSMOE_ERR_INVALID, "gate_up_mid_em: bad shape");
+  if (pairs == 0) return DSMOE_OK;
+  GuEmArgs m{};
+  Shape sd;
+  m.gu = gate_up_args(gate, up, xq, nullptr, weights, nullptr, nullptr, nullptr, mid_out, d, I, k, E, clamp, pairs, &sd);
+  m.sorted_pairs = sorted_pairs;
+  m.offsets = offsets;
+  m.tile_offsets = tile_offsets;
+  m.tile_experts = tile_experts;
+  m.tile_starts = tile_starts;
+  m.tiles = (I + 31) / 32;
+  const int64_t units = (int64_t)(pairs / kEmPairs + std::min(E, pairs)) * m.tiles;
+  if (units > 0x7FFFFFFF) return fail(DSMOE_ERR_UNSUPPORTED, "gate_up_mid_em: too many pairs");
+  return launch(K_UP_EM, dim3((unsigned)units), dim3(256), gate_up_em_lds(d / 256), stream, m);
+}
+
+int dsmoe_down_em(const void* down, const void* mq, const uint32_t* sorted_pairs, const uint32_t* offsets,
+                  const uint32_t* tile_offsets, const uint32_t* tile_experts, const uint32_t* tile_starts,
+                  float* down_out, int32_t d, int32_t I, int32_t E, int32_t pairs, dsmoe_stream_t stream) {
+  if (!down || !mq || !sorted_pairs || !offsets || !tile_offsets || !tile_experts || !tile_starts || !down_out)
+    return fail(DSMOE_ERR_INVALID, "down_em: null pointer");
+  if (!aligned16(down)) return fail(DSMOE_ERR_INVALID, "down_em: weights must be 16-byte aligned");
+  if (d <= 0 || I <= 0 || I % 256 || I > 2048 || E <= 0 || pairs < 0)
+    return fail(I > 2048 ? DSMOE_ERR_UNSUPPORTED : DSMOE_ERR_INVALID, "down_em: bad shape (I a multiple of 256, <= 2048)");
+  if (pairs == 0) return DSMOE_OK;
+  DnEmArgs m{};
+  Shape sd;
+  m.dn = down_args(down, mq, nullptr, down_out, nullptr, d, I, 1, E, 1, &sd);
+  m.sorted_pairs = sorted_pairs;
+  m.offsets = offsets;
+  m.tile_offsets = tile_offsets;
+  m.tile_experts = tile_experts;
+  m.tile_starts = tile_starts;
+  m.tiles = (d + kDnEmRows - 1) / kDnEmRows;
+  const int64_t units = (int64_t)(pairs / kEmPairs + std::min(E, pairs)) * m.tiles;
+  if (units > 0x7FFFFFFF) return fail(DSMOE_ERR_UNSUPPORTED, "down_em: too many pairs");
+  return launch(K_DN_EM, dim3((unsigned)units), dim3(256), down_em_lds(I / 256), stream, m);
 }
 
 int dsmoe_q8_0_gemm(const void* w0, const void* w1, const uint16_t* xh, const float* xscale, float* out, int32_t in_dim,
@@ -768,7 +844,7 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
     if (hipMemset(base, 0, nbytes) != hipSuccess) rc = fail(DSMOE_ERR_HIP, "create: hipMemset of the scratch failed");
   }
   if (max_tokens > kDecodeMaxT && E <= 512) {
-    const size_t P = T * K, max_tiles = P / kGuBM + std::min(E, P);
+    const size_t P = T * K, max_tiles = P / std::min<size_t>(kGuBM, kEmPairs) + std::min(E, P);
     A(&c->xh, T * d * 2);
     A(&c->mh, P * I * 2);
     A(&c->xh80, T * d * 2);
@@ -823,11 +899,15 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // experts as grouped GEMMs over pairs sorted by expert; everything else
   // runs the matvec launches, one work item per (row tile, pair / token).
   const bool grouped = T > kDecodeMaxT && c->xh != nullptr;
+  // Few pairs per expert (at most kEmMaxLoad on average): the routed experts
+  // stream their weights once per chunk of kEmPairs pairs (expert-major
+  // matvec) instead of dequantizing them into MFMA tiles.
+  const bool em = grouped && (int64_t)P <= (int64_t)kEmMaxLoad * E && em_fits(cf);
   // 1. router logits + Q8_K(x) + Q8_0(x)          (session.rs:1894-1909, 1991-2008, 2062-2073)
   {
     StageScope sc(c, DSMOE_STAGE_PREP, stream);
     RouterLogitsArgs r{(const uint16_t*)w->router_f16, x, c->logits, d, E, T};
-    Q8KArgs q8k{x, c->xq8k, d, T, grouped ? c->xh : nullptr};
+    Q8KArgs q8k{x, c->xq8k, d, T, grouped && !em ? c->xh : nullptr};
     Q80Args q80{x, c->xq80, c->xs80, d, T, grouped ? c->xh80 : nullptr};
     DSM_TRY(prep_impl(&r, &q8k, cf.shared_fmt == 0 ? &q80 : nullptr, stream));
   }
@@ -840,8 +920,8 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     StageScope sc(c, DSMOE_STAGE_SELECT, stream);
     DSM_TRY(dsmoe_router_select(&cf, c->logits, w->bias, T, nullptr, sel, wts, stream));
     if (grouped)  // moe_count/prefix/scatter_sorted_pairs + tiles (moe.rs:299-362, 547-596)
-      DSM_TRY(dsmoe_dispatch(sel, P, E, kGuBM, c->g_counts, c->g_offsets, c->g_sorted, c->g_tile_offsets,
-                             c->g_tile_experts, c->g_tile_starts, stream));
+      DSM_TRY(dsmoe_dispatch(sel, P, E, em ? kEmPairs : kGuBM, c->g_counts, c->g_offsets, c->g_sorted,
+                             c->g_tile_offsets, c->g_tile_experts, c->g_tile_starts, stream));
   }
   // 3. routed + shared gate/up/SwiGLU              (session.rs:1910-1959, 2075-2112)
   // The row-streaming launch also quantizes the mid rows (step 4) when the
@@ -864,7 +944,12 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     a.gu_tiles = s1.tiles;
     a.gu_work = grouped ? 0 : P;
     size_t lds = up_rows ? gate_up_rows_lds(nb) : gate_up_lds(nb, s1.R);
-    if (grouped) {
+    if (em) {
+      StageScope sg(c, DSMOE_STAGE_GU_GROUPED, stream);
+      DSM_TRY(dsmoe_gate_up_mid_em(w->gate, w->up, c->xq8k, c->g_sorted, c->g_offsets, c->g_tile_offsets,
+                                   c->g_tile_experts, c->g_tile_starts, wts, c->mid, d, I, K, E, P,
+                                   cf.swiglu_clamp, stream));
+    } else if (grouped) {
       StageScope sg(c, DSMOE_STAGE_GU_GROUPED, stream);
       DSM_TRY(dsmoe_gate_up_mid_sorted(w->gate, w->up, c->xh, c->xq8k, c->g_sorted, c->g_offsets, c->g_tile_offsets,
                                        c->g_tile_experts, c->g_tile_starts, wts, c->mid, d, I, K, E, P,
@@ -903,7 +988,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // 4. Q8_K(mid) + Q8_0 / Q8_K of the shared mid  (session.rs:1964-1976, 2114-2127)
   if (!fuse_midq) {
     StageScope sc(c, DSMOE_STAGE_MIDQ, stream);
-    Q8KArgs qa{c->mid, c->midq, I, P, grouped ? c->mh : nullptr};
+    Q8KArgs qa{c->mid, c->midq, I, P, grouped && !em ? c->mh : nullptr};
     Q8KArgs qb{c->sh_mid, c->sh_midq, Is, T};
     Q80Args q80{c->sh_mid, c->sh_q80, c->sh_s80, Is, T, grouped ? c->shh : nullptr};
     DSM_TRY(midq_impl(&qa, cf.shared_fmt == 1 ? &qb : nullptr, cf.shared_fmt == 0 ? &q80 : nullptr, stream));
@@ -921,8 +1006,13 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     if (grouped) {
       {
         StageScope sg(c, DSMOE_STAGE_DN_GROUPED, stream);
-        DSM_TRY(dsmoe_down_sorted(w->down, c->mh, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets,
-                                  c->g_tile_experts, c->g_tile_starts, c->down_out, d, I, E, P, stream));
+        if (em) {
+          DSM_TRY(dsmoe_down_em(w->down, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets, c->g_tile_experts,
+                                c->g_tile_starts, c->down_out, d, I, E, P, stream));
+        } else {
+          DSM_TRY(dsmoe_down_sorted(w->down, c->mh, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets,
+                                    c->g_tile_experts, c->g_tile_starts, c->down_out, d, I, E, P, stream));
+        }
       }
       DSM_TRY(dsmoe_moe_sum(c->down_out, routed_out, d, K, T, stream));
     }

@@ -145,6 +145,30 @@ struct DnArgs {
   int32_t sh_fmt;
 };
 
+// Expert-major gate/up and down for batches with few pairs per expert: the
+// pairs sorted by expert and cut into chunks of at most kEmPairs pairs of one
+// expert (dsmoe_dispatch with block_m = kEmPairs); grid = max chunks x tiles.
+constexpr int32_t kEmPairs = 8;  // DSMOE_EM_TILE_M
+constexpr int32_t kDnEmRows = 64;  // down rows per expert-major workgroup (8 per step)
+struct GuEmArgs {
+  GateUpArgs gu;  // selected unused; weights per pair; mid_out [pairs][I]
+  const uint32_t* sorted_pairs;
+  const uint32_t* offsets;       // [E + 1]
+  const uint32_t* tile_offsets;  // [E + 1]: chunks = tile_offsets[E]
+  const uint32_t* tile_experts;
+  const uint32_t* tile_starts;
+  int32_t tiles;                 // row tiles of 32 rows
+};
+struct DnEmArgs {
+  DownArgs dn;    // selected and out unused; down_out [pairs][d]
+  const uint32_t* sorted_pairs;
+  const uint32_t* offsets;
+  const uint32_t* tile_offsets;
+  const uint32_t* tile_experts;
+  const uint32_t* tile_starts;
+  int32_t tiles;                 // row tiles of kDnEmRows rows
+};
+
 // Largest token count of the row-streaming (decode) launches.
 constexpr int32_t kMaxDecodeT = 8;
 
@@ -246,6 +270,18 @@ struct DispatchArgs {
 
 // Synthetic weights: N(0, sigma) from a counter-based generator, quantized
 // per 256-element superblock (or 32-element Q8_0 block, or f16/f32 element).
+// Peak probes (dsmoe_probe): what this GPU sustains with no algorithm around
+// it.  kind 0: dense f16 MFMA (v_mfma_f32_32x32x16_f16, eight independent
+// accumulators per wave, `iters` rounds); kind 1: HBM read of `bytes` from
+// `src` with 16-byte loads.  `sink` receives one float per workgroup so the
+// work cannot be dropped.
+struct ProbeArgs {
+  const uint4* src;
+  float* sink;
+  uint64_t n16;   // 16-byte words of src (kind 1)
+  int64_t iters;  // MFMA rounds per wave (kind 0)
+};
+
 struct SynthArgs {
   uint8_t* out;
   const uint8_t* lvlmap;  // IQ2_XXS level-tuple -> grid index map (6561 B)

@@ -110,7 +110,7 @@ __device__ __forceinline__ float iq2_block_dot(const uint32_t* w, const uint8_t*
     }
     const int32_t ls = (int32_t)((aux1 >> 27) | 1u);  // 2 * (aux1 >> 28) + 1
     const int32_t sumi = pos - neg - neg;              // |sumi| <= 32*43*127 < 2^23
-    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(bsum) : "v"(sumi), "v"(ls), "v"(bsum));
+    bsum += __mul24(sumi, ls);  // |sumi| < 2^18, ls <= 31: one v_mad_i32_i24
   }
   const uint32_t dbits = kSecond ? (w[16] >> 16) : (w[0] & 0xFFFF);
   const float xd = f16_to_f32_ftz((uint16_t)dbits);
@@ -874,7 +874,7 @@ __device__ __forceinline__ float iq2_blk_dot(const uint32_t* w, uint32_t sel, ui
     }
     const int32_t ls = (int32_t)((aux1 >> 27) | 1u);
     const int32_t sumi = pos - neg - neg;
-    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(bsum) : "v"(sumi), "v"(ls), "v"(bsum));
+    bsum += __mul24(sumi, ls);  // |sumi| < 2^18, ls <= 31: one v_mad_i32_i24
   }
   const float xd = f16_to_f32_ftz((uint16_t)(w[0] >> dsh));
   return 0.125f * xd * yd * (float)bsum;
@@ -983,6 +983,143 @@ __device__ __forceinline__ void role_gate_up_rows(const GateUpArgs& a, int tile,
     if (a.up_out) a.up_out[off] = uu;
     // device-coherent: a workgroup of this launch may quantize the row block
     stc<true>(a.mid_out + off, (g / (1.0f + expf_dsm(-g))) * uu * wgt);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Expert-major gate/up/SwiGLU (batches with few pairs per expert; the
+// reference's moe_gate_up_mid_sorted_qwarp32, moe.rs:721-815, per-pair
+// arithmetic of :622-715).  A workgroup takes one chunk of up to kEmPairs
+// pairs of one expert (a dsmoe_dispatch tile with block_m = kEmPairs) and 32
+// rows of gate and of up: the weight rows stream once, in the row-streaming
+// layout above (4 lanes per row, lane j takes blocks j, j+4, ...), and every
+// decoded block is multiplied with the activations of all the chunk's pairs,
+// staged in LDS.  The signs go onto the grid bytes before the products
+// (exact: every signed grid byte is in [-43, 43]), so a pair costs two
+// dot4 per 8 weights.  Each pair's sum keeps the reference's order (block
+// classes j and j+4 in-lane, then xor 2, xor 1), so the bits equal the
+// per-pair kernels'.
+// LDS (all dynamic): tables | q8[kEmPairs][nb][272] (each block's d in
+// bytes 256..259 of its padding); the row sums reuse the q8 space after the
+// products.
+// ---------------------------------------------------------------------------
+
+// Signed grid bytes of 8 weights: byte i is -g_i where mask byte i is 0xFF.
+// 0x01010100 - g negates every byte at once (no byte of g is 0, so each
+// byte borrows exactly one from the next).
+__device__ __forceinline__ uint32_t signed_grid4(uint32_t g, uint32_t m) {
+  const uint32_t neg = 0x01010100u - g;
+  return (neg & m) | (g & ~m);
+}
+
+template <int kNit>
+__device__ __forceinline__ void role_gate_up_em(const GuEmArgs& m, int tile, int chunk, uint8_t* smem) {
+  const GateUpArgs& a = m.gu;
+  const int nb = a.d >> 8, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+  if (chunk >= (int)m.tile_offsets[a.E]) return;
+  const int e = (int)m.tile_experts[chunk];
+  const int p0 = (int)(m.offsets[e] + m.tile_starts[chunk]);
+  const int cnt = min(kEmPairs, (int)m.offsets[e + 1] - p0);
+  Iq2Tables* tab = (Iq2Tables*)smem;
+  uint8_t* s_q8 = smem + sizeof(Iq2Tables);  // [kEmPairs][nb][272]
+  float* s_rows = (float*)s_q8;              // [kEmPairs][64], after the products
+
+  const int row0 = tile * 32, mat = wv >> 1, rr = (wv & 1) * 16 + (lane >> 2), j = lane & 3;
+  const int row = min(row0 + rr, a.I - 1);
+  const size_t row_bytes = (size_t)nb * IQ2XXS_BYTES;
+  const uint8_t* wrow = (mat ? a.up : a.gate) + ((size_t)e * a.I + row) * row_bytes;
+  const uint32_t sel = (j & 1) ? 0x07060504u : 0x05040302u, dsh = (j & 1) ? 16u : 0u;
+  uint32_t wb[3][17];
+#pragma unroll
+  for (int i = 0; i < 3 && i < kNit; i++) DSM_BLK_LOAD(wb[i], i)
+  if (tid < 128) tab->mask[tid] = sign_mask64(iq2_sign_byte(tid));
+  tab->grid[tid & 255] = kIq2xxsGrid[tid & 255];
+  // activations of the chunk's pairs: per pair nb * 64 qs words then nb d words
+  const int per = nb * 65;
+  for (int i = tid; i < cnt * per; i += 256) {
+    const int jj = i / per, r = i - jj * per;
+    const uint32_t pair = m.sorted_pairs[p0 + jj];
+    const uint8_t* src = a.xq + (size_t)(pair / (uint32_t)a.k) * nb * Q8K_BYTES;
+    if (r < nb * 64) {
+      *(uint32_t*)(s_q8 + ((size_t)jj * nb + (r >> 6)) * kQ8Stride + 4 * (r & 63)) =
+          *(const uint32_t*)(src + (size_t)(r >> 6) * Q8K_BYTES + 4 + 4 * (r & 63));
+    } else {
+      *(float*)(s_q8 + ((size_t)jj * nb + (r - nb * 64)) * kQ8Stride + 256) = ld_f32(src + (size_t)(r - nb * 64) * Q8K_BYTES);
+    }
+  }
+  __syncthreads();
+
+  float p_lo[kEmPairs], p_hi[kEmPairs];
+#pragma unroll
+  for (int q = 0; q < kEmPairs; q++) { p_lo[q] = 0.0f; p_hi[q] = 0.0f; }
+#pragma unroll
+  for (int i = 0; i < kNit; i++) {
+    const int b = j + 4 * i;
+    if (b < nb) {
+      const uint32_t* w = wb[i % 3];
+      int32_t bsum[kEmPairs];
+#pragma unroll
+      for (int q = 0; q < kEmPairs; q++) bsum[q] = 0;
+#pragma unroll
+      for (int ib = 0; ib < 8; ib++) {
+        const uint32_t aux0 = __builtin_amdgcn_perm(w[2 * ib + 1], w[2 * ib], sel);
+        const uint32_t aux1 = __builtin_amdgcn_perm(w[2 * ib + 2], w[2 * ib + 1], sel);
+        uint32_t sg[8];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const uint64_t gv = tab->grid[(aux0 >> (8 * g)) & 0xFF];
+          const uint64_t mv = tab->mask[(aux1 >> (7 * g)) & 127];
+          sg[2 * g] = signed_grid4((uint32_t)gv, (uint32_t)mv);
+          sg[2 * g + 1] = signed_grid4((uint32_t)(gv >> 32), (uint32_t)(mv >> 32));
+        }
+        const int32_t ls = (int32_t)((aux1 >> 27) | 1u);
+#pragma unroll
+        for (int q = 0; q < kEmPairs; q++) {
+          if (q < cnt) {
+            const uint8_t* q8 = s_q8 + ((size_t)q * nb + b) * kQ8Stride + ib * 32;
+            const uint4 qa = *(const uint4*)q8, qb = *(const uint4*)(q8 + 16);
+            int32_t sumi = dot4(sg[0], qa.x, 0);
+            sumi = dot4(sg[1], qa.y, sumi);
+            sumi = dot4(sg[2], qa.z, sumi);
+            sumi = dot4(sg[3], qa.w, sumi);
+            sumi = dot4(sg[4], qb.x, sumi);
+            sumi = dot4(sg[5], qb.y, sumi);
+            sumi = dot4(sg[6], qb.z, sumi);
+            sumi = dot4(sg[7], qb.w, sumi);
+            bsum[q] += __mul24(sumi, ls);  // |sumi| < 2^18, ls <= 31
+          }
+        }
+      }
+      const float xd = f16_to_f32_ftz((uint16_t)(w[0] >> dsh));
+#pragma unroll
+      for (int q = 0; q < kEmPairs; q++) {
+        if (q < cnt) {
+          const float yd = *(const float*)(s_q8 + ((size_t)q * nb + b) * kQ8Stride + 256);
+          const float v = 0.125f * xd * yd * (float)bsum[q];
+          if (i & 1) p_hi[q] += v; else p_lo[q] += v;
+        }
+      }
+    }
+    if (i + 3 < kNit) DSM_BLK_LOAD(wb[i % 3], i + 3)
+  }
+  __syncthreads();  // every wave is done with the staged activations
+#pragma unroll
+  for (int q = 0; q < kEmPairs; q++) {
+    if (q < cnt) {
+      float v = p_lo[q] + p_hi[q];   // halving tree, level xor 4 (in-lane)
+      v += __shfl_xor(v, 2, 64);     // level xor 2
+      v += __shfl_xor(v, 1, 64);     // level xor 1
+      if (j == 0) s_rows[q * 64 + mat * 32 + rr] = v;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < cnt * 32; i += 256) {
+    const int q = i >> 5, r = i & 31;
+    if (row0 + r >= a.I) continue;
+    const uint32_t pair = m.sorted_pairs[p0 + q];
+    const float g = clamp_gate(s_rows[q * 64 + r], a.clamp), uu = clamp_up(s_rows[q * 64 + 32 + r], a.clamp);
+    const float wgt = a.weights ? a.weights[pair] : 1.0f;
+    a.mid_out[(size_t)pair * a.I + row0 + r] = (g / (1.0f + expf_dsm(-g))) * uu * wgt;
   }
 }
 #undef DSM_BLK_LOAD
@@ -1143,6 +1280,79 @@ __device__ __forceinline__ void role_down_rows(const DownArgs& a, int tile, int 
 }
 __device__ __forceinline__ void role_down_rows_any(const DownArgs& a, int tile, int tok, uint8_t* smem) {
   role_down_rows<1, 2>(a, tile, tok, smem);  // I <= 2048, k <= 8 (checked on the host)
+}
+
+// Expert-major down projection (batches with few pairs per expert;
+// moe_down_sorted_qwarp32, moe.rs:871-916): a workgroup takes one chunk of
+// up to kEmPairs (8) pairs of one expert and kDnEmRows rows of its down
+// matrix, 8 rows per step (2 per wave), the next step's weights in flight
+// during the current one.  Lane l takes pair l/8 of the chunk and block
+// l mod 8 of the row (the reference's lane-strided partial), so the 8 lanes
+// of a block read the same weight bytes; the 8-lane butterfly finishes each
+// pair's row and the value goes to down_out[pair][row] (the slot-ordered sum
+// runs after, in dsmoe_moe_sum).  I <= 2048 (one block per lane).
+// LDS: yd[kEmPairs*nb] | bsums[kEmPairs*nb][16] | q8[kEmPairs*nb][272]
+__device__ __forceinline__ void role_down_em(const DnEmArgs& m, int tile, int chunk, uint8_t* smem) {
+  const DownArgs& a = m.dn;
+  const int nb = a.I >> 8, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+  if (chunk >= (int)m.tile_offsets[a.E]) return;
+  const int e = (int)m.tile_experts[chunk];
+  const int p0 = (int)(m.offsets[e] + m.tile_starts[chunk]);
+  const int cnt = min(kEmPairs, (int)m.offsets[e + 1] - p0);
+  float* s_yd = (float*)smem;
+  int16_t* s_bs = (int16_t*)(s_yd + align_up(kEmPairs * nb, 4));
+  uint8_t* s_q8 = (uint8_t*)(s_bs + kEmPairs * nb * 16);
+  const int q = lane >> 3, j = lane & 7;
+  constexpr int kSteps = kDnEmRows / 8;
+  const size_t row_bytes = (size_t)nb * Q2K_BYTES;
+  const int row0 = tile * kDnEmRows;
+  const uint8_t* wbase = a.down + (size_t)e * a.d * row_bytes + (size_t)min(j, nb - 1) * Q2K_BYTES;
+  auto load = [&](int st, uint32_t (&w)[2][21]) {
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int row = min(row0 + 8 * st + wv + 4 * r, a.d - 1);
+      const uint8_t* src = wbase + (size_t)row * row_bytes;
+#pragma unroll
+      for (int c = 0; c < 5; c++) {
+        const uint4 v4 = *(const uint4*)(src + 16 * c);
+        w[r][4 * c] = v4.x; w[r][4 * c + 1] = v4.y; w[r][4 * c + 2] = v4.z; w[r][4 * c + 3] = v4.w;
+      }
+      w[r][20] = *(const uint32_t*)(src + 80);
+    }
+  };
+  uint32_t wa[2][21], wb[2][21];
+  load(0, wa);
+  // the chunk's Q8_K(mid) blocks: per block 64 qs words, 1 d word, 8 bsums words
+  const int nblk = cnt * nb;
+  for (int i = tid; i < nblk * 73; i += 256) {
+    const int blk = i / 73, r = i - blk * 73, qq = blk / nb, b = blk - qq * nb;
+    const uint32_t pair = m.sorted_pairs[p0 + qq];
+    const uint8_t* src = a.midq + ((size_t)pair * nb + b) * Q8K_BYTES;
+    if (r < 64) *(uint32_t*)(s_q8 + (size_t)blk * kQ8Stride + 4 * r) = *(const uint32_t*)(src + 4 + 4 * r);
+    else if (r == 64) s_yd[blk] = ld_f32(src);
+    else ((uint32_t*)s_bs)[blk * 8 + (r - 65)] = *(const uint32_t*)(src + 260 + 4 * (r - 65));
+  }
+  __syncthreads();
+  const bool live = q < cnt && j < nb;
+  const int qb = q * nb + j;
+  const uint32_t pair = m.sorted_pairs[p0 + min(q, cnt - 1)];
+  auto run = [&](int st, const uint32_t (&w)[2][21]) {
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      float p = 0.0f;  // the reference's lane-strided partial j of this pair's row
+      if (live) p = q2k_block_dot(w[r], s_q8 + qb * kQ8Stride, s_bs + qb * 16, s_yd[qb]);
+      p = group_sum<8>(p);
+      const int row = row0 + 8 * st + wv + 4 * r;
+      if (j == 0 && q < cnt && row < a.d) a.down_out[(size_t)pair * a.d + row] = p;
+    }
+  };
+#pragma unroll
+  for (int st = 0; st < kSteps; st += 2) {
+    load(min(st + 1, kSteps - 1), wb);
+    run(st, wa);
+    load(min(st + 2, kSteps - 1), wa);
+    run(st + 1, wb);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1774,6 +1984,29 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_dn_rows(const DnArgs a) 
     if (a.sh_fmt == 0) role_q80_rows_any(a.sh_q80, w % a.sh_tiles, w / a.sh_tiles, smem);
     else role_down<false>(a.sh_q2k, w % a.sh_tiles, w / a.sh_tiles, smem);
   }
+}
+
+// Expert-major gate/up and down (batches with few pairs per expert):
+// workgroup = (row tile, dispatch chunk); chunks past the dispatch's count
+// return at once.
+extern "C" __global__ __launch_bounds__(256) void dsmoe_up_em(const GuEmArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tile = blockIdx.x % a.tiles, chunk = blockIdx.x / a.tiles;
+  switch ((a.gu.d + 1023) >> 10) {  // blocks per lane (d <= 8192)
+    case 1: role_gate_up_em<1>(a, tile, chunk, smem); break;
+    case 2: role_gate_up_em<2>(a, tile, chunk, smem); break;
+    case 3: role_gate_up_em<3>(a, tile, chunk, smem); break;
+    case 4: role_gate_up_em<4>(a, tile, chunk, smem); break;
+    case 5: role_gate_up_em<5>(a, tile, chunk, smem); break;
+    case 6: role_gate_up_em<6>(a, tile, chunk, smem); break;
+    case 7: role_gate_up_em<7>(a, tile, chunk, smem); break;
+    default: role_gate_up_em<8>(a, tile, chunk, smem); break;
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void dsmoe_dn_em(const DnEmArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  role_down_em(a, blockIdx.x % a.tiles, blockIdx.x / a.tiles, smem);
 }
 
 extern "C" __global__ __launch_bounds__(256) void dsmoe_router_select(const RouterSelectArgs a) {

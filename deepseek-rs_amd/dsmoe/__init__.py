@@ -25,7 +25,7 @@ IQ2XXS_BYTES, Q2K_BYTES, Q8K_BYTES, Q8_0_BYTES = 66, 84, 292, 34
 
 EXPORTED = [
     "dsmoe_version", "dsmoe_last_error", "dsmoe_init", "dsmoe_create", "dsmoe_destroy",
-    "dsmoe_scratch_bytes", "dsmoe_forward", "dsmoe_forward_noalloc", "dsmoe_hc_expand", "dsmoe_router_logits", "dsmoe_router_select",
+    "dsmoe_scratch_bytes", "dsmoe_forward", "dsmoe_forward_noalloc", "dsmoe_hc_expand", "dsmoe_probe", "dsmoe_gate_up_mid_em", "dsmoe_down_em", "dsmoe_router_logits", "dsmoe_router_select",
     "dsmoe_q8k_quantize", "dsmoe_q8_0_quantize", "dsmoe_gate_up_mid", "dsmoe_down", "dsmoe_moe_sum",
     "dsmoe_q8_0_matvec", "dsmoe_swiglu", "dsmoe_dispatch", "dsmoe_tensor_bytes", "dsmoe_synth_tensor",
     "dsmoe_synth_tensor_host", "dsmoe_stage_name", "dsmoe_set_profiling", "dsmoe_profile_read",
@@ -74,6 +74,9 @@ def lib():
         "dsmoe_destroy": ([vp], i32),
         "dsmoe_scratch_bytes": ([vp], ctypes.c_size_t),
         "dsmoe_forward": ([vp, ctypes.POINTER(Weights), vp, i32, vp, vp, vp, vp, vp], i32),
+        "dsmoe_gate_up_mid_em": ([vp] * 10 + [i32, i32, i32, i32, i32, f32, vp], i32),
+        "dsmoe_down_em": ([vp] * 8 + [i32, i32, i32, i32, vp], i32),
+        "dsmoe_probe": ([i32, vp, ctypes.c_size_t, ctypes.c_int64, vp, vp], i32),
         "dsmoe_hc_expand": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp], i32),
         "dsmoe_forward_noalloc": ([ctypes.POINTER(Config), ctypes.POINTER(Weights), vp, i32, vp, vp, vp, vp, vp], i32),
         "dsmoe_router_logits": ([vp, vp, vp, i32, i32, i32, vp], i32),
@@ -299,6 +302,29 @@ def hc_expand(block_out, block_add, residual_hc, split, out_hc, n_embd, n_hc, T,
     """hc_expand (hc.rs:212-259): the residual merge after the layer."""
     check(lib().dsmoe_hc_expand(_p(block_out), _p(block_add), _p(residual_hc), _p(split), _p(out_hc), n_embd, n_hc, T,
                                 mix_hc, int(has_add), _stream(stream)))
+
+
+EM_TILE_M = 8
+
+
+def gate_up_mid_em(gate, up, xq, sorted_pairs, offsets, tile_offsets, tile_experts, tile_starts, weights, mid_out,
+                   d, I, k, E, pairs, clamp, stream=None):
+    """Expert-major gate/up/SwiGLU over pairs dispatched with block_m = EM_TILE_M (moe.rs:721-815)."""
+    check(lib().dsmoe_gate_up_mid_em(_p(gate), _p(up), _p(xq), _p(sorted_pairs), _p(offsets), _p(tile_offsets),
+                                     _p(tile_experts), _p(tile_starts), _p(weights), _p(mid_out), d, I, k, E, pairs,
+                                     clamp, _stream(stream)))
+
+
+def down_em(w, mq, sorted_pairs, offsets, tile_offsets, tile_experts, tile_starts, down_out, d, I, E, pairs,
+            stream=None):
+    """Expert-major down over pairs dispatched with block_m = EM_TILE_M (moe.rs:871-916)."""
+    check(lib().dsmoe_down_em(_p(w), _p(mq), _p(sorted_pairs), _p(offsets), _p(tile_offsets), _p(tile_experts),
+                              _p(tile_starts), _p(down_out), d, I, E, pairs, _stream(stream)))
+
+
+def probe(kind, src, nbytes, iters, sink, stream=None):
+    """dsmoe_probe: kind 0 = dense f16 MFMA loop, 1 = HBM read of nbytes of src."""
+    check(lib().dsmoe_probe(int(kind), _p(src), int(nbytes), int(iters), _p(sink), _stream(stream)))
 
 
 def forward_noalloc(cfg, w, x, shared_out, routed_out, selected=None, weights=None, stream=None):

@@ -199,6 +199,26 @@ int dsmoe_gate_up_mid_sorted(const void* gate, const void* up, const uint16_t* x
                              float* mid_out, int32_t d, int32_t I, int32_t k, int32_t E, int32_t pairs, float clamp,
                              dsmoe_stream_t stream);
 
+/* moe_gate_up_mid_sorted_qwarp32 (engine/src/kernels/moe.rs:721-815) in
+ * the expert-major matvec form, for batches with few pairs per expert: the
+ * pairs grouped by dsmoe_dispatch with block_m = DSMOE_EM_TILE_M; every
+ * expert's weight rows stream once per tile of up to 8 pairs, each decoded
+ * block multiplied with all the tile's activations.  xq: Q8_K(x).  Same bits
+ * as dsmoe_gate_up_mid.  d a multiple of 512, at most 7168. */
+#define DSMOE_EM_TILE_M 8
+int dsmoe_gate_up_mid_em(const void* gate, const void* up, const void* xq, const uint32_t* sorted_pairs,
+                         const uint32_t* offsets, const uint32_t* tile_offsets, const uint32_t* tile_experts,
+                         const uint32_t* tile_starts, const float* weights, float* mid_out, int32_t d, int32_t I,
+                         int32_t k, int32_t E, int32_t pairs, float clamp, dsmoe_stream_t stream);
+
+/* moe_down_sorted_qwarp32 (moe.rs:871-916) in the expert-major form:
+ * down_out[pair][row] for the pairs grouped by dsmoe_dispatch with block_m =
+ * DSMOE_EM_TILE_M; mq: Q8_K(mid).  Same bits as dsmoe_down's per-pair
+ * values; the slot sum is dsmoe_moe_sum.  I at most 2048. */
+int dsmoe_down_em(const void* down, const void* mq, const uint32_t* sorted_pairs, const uint32_t* offsets,
+                  const uint32_t* tile_offsets, const uint32_t* tile_experts, const uint32_t* tile_starts,
+                  float* down_out, int32_t d, int32_t I, int32_t E, int32_t pairs, dsmoe_stream_t stream);
+
 /* moe_down_sorted_qwarp32 (engine/src/kernels/moe.rs:821-916, sorted
  * variant): down_out[pair][row] for the pairs grouped by dsmoe_dispatch
  * (block_m = DSMOE_GROUPED_TILE_M), the per-pair values dsmoe_down computes
@@ -218,6 +238,14 @@ int dsmoe_down(const void* down, const void* midq, const int32_t* selected, floa
 
 /* moe_sum (engine/src/kernels/moe.rs:983-1005). */
 int dsmoe_moe_sum(const float* down, float* out, int32_t d, int32_t k, int32_t T, dsmoe_stream_t stream);
+
+/* Peak probes, no reference counterpart (measurement support for the
+ * benchmark).  kind 0: dense f16 MFMA, 2 workgroups of 4 waves per CU, each
+ * wave `iters` rounds of 8 independent v_mfma_f32_32x32x16_f16 (32768 flops
+ * each).  kind 1: one read of `bytes` of `src` (device, 16-byte aligned)
+ * with 16-byte loads, 8 workgroups per CU.  `sink` (device, >= 8 floats per
+ * CU) is written only on a data-dependent branch. */
+int dsmoe_probe(int32_t kind, const void* src, size_t bytes, int64_t iters, float* sink, dsmoe_stream_t stream);
 
 /* hc_expand (engine/src/kernels/hc.rs:212-259), the FFN residual merge that
  * consumes the layer's outputs (session.rs:2157-2175: block_out =

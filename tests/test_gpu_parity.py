@@ -299,6 +299,56 @@ def test_gate_up_sorted_matches_per_pair(gpu, d, I, E, T, k, skew, big):
     assert bits_equal(np_(dd), np_(dd_ref))
 
 
+@pytest.mark.parametrize("d,I,E,T,k,skew", [(7168, 2048, 16, 40, 8, True), (7168, 2048, 256, 32, 8, False),
+                                             (2048, 1536, 8, 5, 3, False), (1024, 512, 3, 9, 2, True)])
+def test_expert_major_matches_per_pair(gpu, d, I, E, T, k, skew):
+    """The expert-major gate/up and down (pairs dispatched in tiles of 8, each
+    expert's rows streamed once per tile) must give the per-pair kernels'
+    bits: hot experts with several tiles, cold ones with one pair."""
+    import torch
+    say(f"expert-major d={d} I={I} E={E} T={T} k={k} skew={skew}")
+    rng = np.random.default_rng(d + I + T + 1)
+    gate = dsmoe.synth(dsmoe.FMT_IQ2_XXS, 4, 1, E, I, d, sigma=0.02, device=gpu)
+    up = dsmoe.synth(dsmoe.FMT_IQ2_XXS, 4, 2, E, I, d, sigma=0.02, device=gpu)
+    dn = dsmoe.synth(dsmoe.FMT_Q2_K, 4, 3, E, d, I, sigma=0.02, device=gpu)
+    x = dsmoe.synth(dsmoe.FMT_F32, 4, 4, 1, T, d, sigma=1.0, device=gpu)
+    if skew:
+        p = np.array([0.5 ** i for i in range(E)])
+        p /= p.sum()
+        sel = np.stack([rng.choice(E, k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+    else:
+        sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    w = rng.uniform(0.1, 0.5, (T, k)).astype(np.float32)
+    P_ = T * k
+    dsel = torch.from_numpy(sel.reshape(-1)).to(gpu)
+    dw = torch.from_numpy(w.reshape(-1)).to(gpu)
+    xq = torch.empty(T * (d // 256) * 292, dtype=torch.uint8, device=gpu)
+    dsmoe.q8k_quantize(x, xq, d, T)
+    m_ref = torch.empty(P_, I, device=gpu)
+    dsmoe.gate_up_mid(gate, up, xq, dsel, dw, None, None, m_ref, d, I, T, k, E, 10.0)
+    u32 = dict(dtype=torch.int32, device=gpu)
+    counts, offsets = torch.empty(E, **u32), torch.empty(E + 1, **u32)
+    sp = torch.empty(P_, **u32)
+    max_tiles = P_ // dsmoe.EM_TILE_M + min(E, P_)
+    toff, texp, tst = torch.empty(E + 1, **u32), torch.empty(max_tiles, **u32), torch.empty(max_tiles, **u32)
+    dsmoe.dispatch(dsel, P_, E, dsmoe.EM_TILE_M, counts, offsets, sp, toff, texp, tst)
+    m = torch.full((P_, I), float("nan"), device=gpu)
+    dsmoe.gate_up_mid_em(gate, up, xq, sp, offsets, toff, texp, tst, dw, m, d, I, k, E, P_, 10.0)
+    torch.cuda.synchronize()
+    say(f"  tiles={int(np_(toff)[-1])} max_count={int(np_(counts).max())}")
+    assert_close(np_(m).reshape(-1), np_(m_ref).reshape(-1), "mid expert-major vs per-pair")
+    assert bits_equal(np_(m), np_(m_ref))
+    mq = torch.empty(P_ * (I // 256) * 292, dtype=torch.uint8, device=gpu)
+    dsmoe.q8k_quantize(m_ref, mq, I, P_)
+    dd_ref = torch.empty(P_, d, device=gpu)
+    dsmoe.down(dn, mq, dsel, dd_ref, None, d, I, T, k, E)
+    dd = torch.full((P_, d), float("nan"), device=gpu)
+    dsmoe.down_em(dn, mq, sp, offsets, toff, texp, tst, dd, d, I, E, P_)
+    torch.cuda.synchronize()
+    assert_close(np_(dd).reshape(-1), np_(dd_ref).reshape(-1), "down expert-major vs per-pair")
+    assert bits_equal(np_(dd), np_(dd_ref))
+
+
 @pytest.mark.parametrize("din,dout,T", [(7168, 2048, 130), (2048, 1408, 64), (1408, 2048, 9), (2048, 7168, 70),
                                          (4096, 1024, 33)])
 def test_q8_0_gemm_matches_matvec(gpu, din, dout, T):
