@@ -112,34 +112,36 @@ __device__ __forceinline__ int class_len(int ci, int nb) {
 }
 
 // Work mapping for a 1-D grid of 8 * ceil(tiles / 8) * ny workgroups.  The
-// dispatcher hands workgroup h to XCD h mod 8 (each XCD has its own L2), so
-// the (tile, slab) pairs are laid out such that each XCD gets a contiguous
-// run of ceil(ntiles / 8) tiles and all ny slabs of one tile back to back:
-// the tile's activations are then fetched into that XCD's L2 once and reused
-// by every slab.  Any dispatch order still covers each (tile, slab) exactly
-// once; only the cache reuse depends on it.
+// dispatcher hands workgroup h to XCD h mod 8 (each XCD has its own L2).
+// With at least 8 tiles each XCD gets a contiguous run of ceil(ntiles / 8)
+// tiles: xcd_tile_slab puts all ny slabs of one tile back to back (the
+// tile's activations are fetched into that XCD's L2 once and reused by every
+// slab), xcd_slab_tile puts the slabs outermost (for dense GEMMs over a token
+// batch a weight slab is then read once per XCD while the XCD's tiles of
+// activations stay in its L2).  With fewer than 8 tiles that would leave
+// XCDs idle, so the ntiles * ny items are cut into 8 equal runs instead.
+// Any dispatch order still covers each (tile, slab) exactly once; only the
+// cache reuse depends on it.  ntiles may be below the count the grid was
+// sized for (the dispatch's tile count is read on the device): the extra
+// workgroups return.
 struct TileSlab {
   int t, n;
   bool ok;
 };
-__device__ __forceinline__ TileSlab xcd_tile_slab(int ntiles, int ny) {
+__device__ __forceinline__ TileSlab xcd_items(int ntiles, int ny, bool slab_major) {
   const int h = blockIdx.x, xcd = h & 7, s = h >> 3;
-  const int k = s / ny, n = s - k * ny;
+  if (ntiles < 8) {
+    const int W = ntiles * ny, per = (W + 7) >> 3, i = xcd * per + s;
+    if (s >= per || i >= W) return {0, 0, false};
+    return slab_major ? TileSlab{i % ntiles, i / ntiles, true} : TileSlab{i / ny, i % ny, true};
+  }
   const int chunk = (ntiles + 7) >> 3;
+  const int k = slab_major ? s % chunk : s / ny, n = slab_major ? s / chunk : s - (s / ny) * ny;
   const int t = xcd * chunk + k;
-  return {t, n, k < chunk && t < ntiles};
+  return {t, n, n < ny && k < chunk && t < ntiles};
 }
-
-// The same grid with the slabs outermost inside each XCD's run of tiles: for
-// few tiles per XCD (dense GEMMs over a token batch) a weight slab is then
-// read once per XCD while the XCD's tiles of activations stay in its L2.
-__device__ __forceinline__ TileSlab xcd_slab_tile(int ntiles, int ny) {
-  const int h = blockIdx.x, xcd = h & 7, s = h >> 3;
-  const int chunk = (ntiles + 7) >> 3;
-  const int k = s % chunk, n = s / chunk;
-  const int t = xcd * chunk + k;
-  return {t, n, n < ny && t < ntiles};
-}
+__device__ __forceinline__ TileSlab xcd_tile_slab(int ntiles, int ny) { return xcd_items(ntiles, ny, false); }
+__device__ __forceinline__ TileSlab xcd_slab_tile(int ntiles, int ny) { return xcd_items(ntiles, ny, true); }
 
 }  // namespace
 
@@ -710,10 +712,12 @@ __device__ __forceinline__ void q80_gemm(const Q80GemmArgs& a, Q80Smem& sm) {
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int in = a.in_dim, nb = in >> 5, T = a.T;
-  const TileSlab ts = xcd_slab_tile((T + kGuBM - 1) / kGuBM, a.out_dim / (kSwiglu ? 32 : 64));
+  const int S = a.ksplit;
+  const TileSlab ts = xcd_slab_tile((T + kGuBM - 1) / kGuBM, a.out_dim / (kSwiglu ? 32 : 64) * S);
   if (!ts.ok) return;
   const int m0 = ts.t * kGuBM;
-  const int n0 = ts.n * (kSwiglu ? 32 : 64);
+  const int n0 = (ts.n / S) * (kSwiglu ? 32 : 64), split = ts.n % S;
+  const int kb = split * (32 / S), ke = kb + 32 / S;  // class positions of this workgroup
 
   // A stage holds up to 8 blocks: G = 8 / jmax lane classes of jmax slots
   // each (jmax = blocks of the longest class); slot u = class position
@@ -813,12 +817,12 @@ __device__ __forceinline__ void q80_gemm(const Q80GemmArgs& a, Q80Smem& sm) {
     for (int i = 0; i < 16; i++) run[i] = 0.0f;
   };
 
-  DSM_Q80_ISSUE(0)
-  for (int k0 = 0; k0 < 32; k0 += G) {
+  DSM_Q80_ISSUE(kb)
+  for (int k0 = kb; k0 < ke; k0 += G) {
     __syncthreads();
     DSM_Q80_COMMIT(k0)
-    // past the end: re-read stage 0 (unused); unconditional loads keep the wait counts exact
-    DSM_Q80_ISSUE(k0 + G < 32 ? k0 + G : 0)
+    // past the end: re-read the first stage (unused); unconditional loads keep the wait counts exact
+    DSM_Q80_ISSUE(k0 + G < ke ? k0 + G : kb)
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < 8; u++) {
@@ -841,12 +845,24 @@ __device__ __forceinline__ void q80_gemm(const Q80GemmArgs& a, Q80Smem& sm) {
           run[i] = run[i] + (sw * s_xs[u][m]) * acc[i];
         }
       }
-      if (j == jmax - 1) fold(k);
+      if (j == jmax - 1) fold(k - kb);
     }
   }
 
 #undef DSM_Q80_ISSUE
 #undef DSM_Q80_COMMIT
+  if (S > 1) {
+    // the subtree of this workgroup's 32 / S classes: lv[log2(32 / S)]
+    const float16v& sub = S == 2 ? lv4 : S == 4 ? lv3 : S == 8 ? lv2 : lv1;
+    const int cols = kSwiglu ? 2 * a.out_dim : a.out_dim;
+    const int col = kSwiglu ? nt * a.out_dim + n0 + (lane & 31) : n0 + nt * 32 + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int m = m0 + mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+      if (m < T) a.part[((size_t)split * T + m) * cols + col] = sub[i];
+    }
+    return;
+  }
   if (!kSwiglu) {
 #pragma unroll
     for (int i = 0; i < 16; i++) {
@@ -1012,4 +1028,27 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_probe_read(const ProbeAr
     x ^= v.x ^ v.y ^ v.z ^ v.w;
   }
   if (x == 0x9E3779B9u) a.sink[blockIdx.x] = (float)x;  // data-dependent, almost never taken
+}
+
+// Finishes a split Q8_0 GEMM: the partial sums of the ksplit class groups
+// added pairwise in split order (for ksplit = 2^s the groups are the subtrees
+// of the halving tree's top s levels, in tree order), then SwiGLU (weight 1)
+// when the GEMM had gate and up.  One thread per output.
+extern "C" __global__ __launch_bounds__(256) void dsmoe_q80_combine(const Q80CombineArgs a) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)a.T * a.out_dim) return;
+  const size_t t = i / a.out_dim, c = i % a.out_dim;
+  const int cols = a.two ? 2 * a.out_dim : a.out_dim;
+  const size_t plane = (size_t)a.T * cols;
+  auto tree = [&](size_t col) {
+    float v[8];
+    for (int s = 0; s < a.ksplit; s++) v[s] = a.part[s * plane + t * cols + col];
+    for (int w = a.ksplit; w > 1; w >>= 1)
+      for (int s = 0; s < w / 2; s++) v[s] = v[2 * s] + v[2 * s + 1];
+    return v[0];
+  };
+  const float g0 = tree(c);
+  if (!a.two) { a.out[i] = g0; return; }
+  const float g = clamp_gate(g0, a.clamp), u = clamp_up(tree(a.out_dim + c), a.clamp);
+  a.out[i] = (g / (1.0f + expf_dsm(-g))) * u * 1.0f;
 }

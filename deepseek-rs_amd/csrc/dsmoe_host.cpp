@@ -84,16 +84,17 @@ const std::vector<uint8_t>& lvlmap_host() {
 enum Kern { K_PREP, K_ROUTER_SELECT, K_UP, K_MIDQ, K_DN, K_SWIGLU, K_MOE_SUM, K_DISPATCH, K_SYNTH,
             K_GU_GROUPED, K_DN_GROUPED, K_Q80_GEMM_SWIGLU, K_Q80_GEMM,
             K_ROUTER_TILE, K_UP_ROWS, K_DN_ROWS, K_Q80_GEMM_SWIGLU_J7, K_Q80_GEMM_J7, K_Q80_GEMM_SWIGLU_J2,
-            K_Q80_GEMM_J2, K_HC_EXPAND, K_PROBE_MFMA, K_PROBE_READ, K_UP_EM, K_DN_EM, K_COUNT };
+            K_Q80_GEMM_J2, K_HC_EXPAND, K_PROBE_MFMA, K_PROBE_READ, K_UP_EM, K_DN_EM, K_Q80_COMBINE, K_COUNT };
 const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_up", "dsmoe_midq", "dsmoe_dn",
                                    "dsmoe_swiglu", "dsmoe_moe_sum", "dsmoe_dispatch", "dsmoe_synth",
                                    "dsmoe_gu_grouped", "dsmoe_dn_grouped", "dsmoe_q80_gemm_swiglu", "dsmoe_q80_gemm",
                                    "dsmoe_router_tile",
                                    "dsmoe_up_rows", "dsmoe_dn_rows", "dsmoe_q80_gemm_swiglu_j7", "dsmoe_q80_gemm_j7",
                                    "dsmoe_q80_gemm_swiglu_j2", "dsmoe_q80_gemm_j2", "dsmoe_hc_expand",
-                                   "dsmoe_probe_mfma", "dsmoe_probe_read", "dsmoe_up_em", "dsmoe_dn_em"};
+                                   "dsmoe_probe_mfma", "dsmoe_probe_read", "dsmoe_up_em", "dsmoe_dn_em",
+                                   "dsmoe_q80_combine"};
 // code object of each kernel: 0 = dsmoe_kernels.hsaco, 1 = dsmoe_gemm.hsaco (same directory)
-const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0, 1, 1, 0, 0};
+const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0, 1, 1, 0, 0, 1};
 static_assert(DSMOE_GROUPED_TILE_M == kGuBM, "header and kernels disagree on the grouped tile");
 
 extern "C" int dsmoe_noalloc_setup(void** ptr, size_t* bytes);  // dsmoe_noalloc.hip
@@ -178,8 +179,25 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // the workgroup (<= 1024 threads) and the grid has at least ~2 workgroups
 // per CU (256 CUs).
 constexpr int kMinWgs = 512;
-constexpr int kDecodeMaxT = kMaxDecodeT;
-constexpr int kEmMaxLoad = 4;  // pairs per expert (on average) up to which batches run expert-major  // row-streaming (matvec) launches up to 8 tokens, grouped GEMMs above
+constexpr int kDecodeMaxT = kMaxDecodeT;  // row-streaming (matvec) launches up to 8 tokens, batch paths above
+constexpr int kEmMaxLoad = 4;
+constexpr int kQ80MaxSplit = 8;  // class groups of a split shared-expert GEMM (up to 256 tokens)  // pairs per expert (on average) up to which batches run expert-major
+#ifdef DSM_PROBE
+// measurement builds only: launch-shape overrides from the environment
+int dsm_tune(const char* name, int def) {
+  const char* v = getenv(name);
+  return v ? atoi(v) : def;
+}
+#define DSM_TUNE(name, def) dsm_tune(name, def)
+#else
+#define DSM_TUNE(name, def) (def)
+#endif
+// Pairs per expert-major chunk: a chunk keeps its activations in LDS, so a
+// smaller chunk leaves room for more workgroups per compute unit, a larger
+// one streams a busy expert's rows fewer times.  4 measured best on c3
+// (T = 32, about 1.5 pairs per used expert) and c4 (T = 128, about 4)
+// against 1, 2 and 8.
+int em_pairs() { return DSM_TUNE("DSM_EM_NP", 4); }
 
 int pow2_floor(int v) {
   int p = 1;
@@ -226,9 +244,9 @@ int select_wave_p(const dsmoe_config& cf) {
   return 0;
 }
 // Expert-major launches (dsmoe_up_em / dsmoe_dn_em): shapes they take.  The
-// gate/up workgroup stages kEmPairs activations in at most 61 KB of LDS.
-size_t gate_up_em_lds(int nb) { return 3072 + (size_t)kEmPairs * nb * 272; }
-size_t down_em_lds(int nb) { return (size_t)((kEmPairs * nb + 3) / 4 * 4) * 4 + (size_t)kEmPairs * nb * (32 + 272); }
+// gate/up workgroup stages up to kEmPairs activations in LDS (at most 64 KB).
+size_t gate_up_em_lds(int nb, int np = kEmPairs) { return 3072 + (size_t)np * nb * 272; }
+size_t down_em_lds(int nb, int np = kEmPairs) { return (size_t)np * nb * 304; }
 bool em_fits(const dsmoe_config& cf) {
   return up_rows_fits(cf.d_model) && gate_up_em_lds(cf.d_model / 256) <= 64 * 1024 && cf.d_ff <= 2048 &&
          cf.d_ff % 256 == 0;
@@ -553,7 +571,8 @@ int dsmoe_dispatch(const int32_t* selected, int32_t pairs, int32_t E, int32_t bl
 }
 
 // 1-D grid of the grouped kernels: ny slabs for each of 8 * ceil(tiles / 8)
-// tile slots (the kernels' xcd_tile_slab mapping).
+// tile slots (the kernels' xcd_items mapping; it also covers the tiles x ny
+// items of a grid with fewer than 8 tiles).
 static unsigned xcd_grid(int tiles, int ny) { return 8u * (unsigned)((tiles + 7) / 8) * (unsigned)ny; }
 
 int dsmoe_gate_up_mid_sorted(const void* gate, const void* up, const uint16_t* xh, const void* xq,
@@ -595,13 +614,14 @@ int dsmoe_down_sorted(const void* down, const uint16_t* mh, const void* mq, cons
 int dsmoe_gate_up_mid_em(const void* gate, const void* up, const void* xq, const uint32_t* sorted_pairs,
                          const uint32_t* offsets, const uint32_t* tile_offsets, const uint32_t* tile_experts,
                          const uint32_t* tile_starts, const float* weights, float* mid_out, int32_t d, int32_t I,
-                         int32_t k, int32_t E, int32_t pairs, float clamp, dsmoe_stream_t stream) {
+                         int32_t k, int32_t E, int32_t pairs, int32_t block_m, float clamp, dsmoe_stream_t stream) {
   if (!gate || !up || !xq || !sorted_pairs || !offsets || !tile_offsets || !tile_experts || !tile_starts || !mid_out)
     return fail(DSMOE_ERR_INVALID, "gate_up_mid_em: null pointer");
   if (!aligned16(gate) || !aligned16(up)) return fail(DSMOE_ERR_INVALID, "gate_up_mid_em: weights must be 16-byte aligned");
-  if (!up_rows_fits(d) || gate_up_em_lds(d / 256) > 64 * 1024)
-    return fail(DSMOE_ERR_UNSUPPORTED, "gate_up_mid_em: d must be a multiple of 512, at most 7168");
   if (I <= 0 || k <= 0 || E <= 0 || pairs < 0) return fail(DSMOE_ERR_INVALID, "gate_up_mid_em: bad shape");
+  if (block_m < 1 || block_m > kEmPairs) return fail(DSMOE_ERR_INVALID, "gate_up_mid_em: block_m must be in 1..8");
+  if (!up_rows_fits(d) || gate_up_em_lds(d / 256, block_m) > 64 * 1024)
+    return fail(DSMOE_ERR_UNSUPPORTED, "gate_up_mid_em: d must be a multiple of 512 whose block_m activations fit 64 KB");
   if (pairs == 0) return DSMOE_OK;
   GuEmArgs m{};
   Shape sd;
@@ -612,19 +632,22 @@ int dsmoe_gate_up_mid_em(const void* gate, const void* up, const void* xq, const
   m.tile_experts = tile_experts;
   m.tile_starts = tile_starts;
   m.tiles = (I + 31) / 32;
-  const int64_t units = (int64_t)(pairs / kEmPairs + std::min(E, pairs)) * m.tiles;
+  m.np = block_m;
+  const int64_t units = (int64_t)(pairs / block_m + std::min(E, pairs)) * m.tiles;
   if (units > 0x7FFFFFFF) return fail(DSMOE_ERR_UNSUPPORTED, "gate_up_mid_em: too many pairs");
-  return launch(K_UP_EM, dim3((unsigned)units), dim3(256), gate_up_em_lds(d / 256), stream, m);
+  return launch(K_UP_EM, dim3((unsigned)units), dim3(256), gate_up_em_lds(d / 256, block_m), stream, m);
 }
 
 int dsmoe_down_em(const void* down, const void* mq, const uint32_t* sorted_pairs, const uint32_t* offsets,
                   const uint32_t* tile_offsets, const uint32_t* tile_experts, const uint32_t* tile_starts,
-                  float* down_out, int32_t d, int32_t I, int32_t E, int32_t pairs, dsmoe_stream_t stream) {
+                  float* down_out, int32_t d, int32_t I, int32_t E, int32_t pairs, int32_t block_m,
+                  dsmoe_stream_t stream) {
   if (!down || !mq || !sorted_pairs || !offsets || !tile_offsets || !tile_experts || !tile_starts || !down_out)
     return fail(DSMOE_ERR_INVALID, "down_em: null pointer");
   if (!aligned16(down)) return fail(DSMOE_ERR_INVALID, "down_em: weights must be 16-byte aligned");
   if (d <= 0 || I <= 0 || I % 256 || I > 2048 || E <= 0 || pairs < 0)
     return fail(I > 2048 ? DSMOE_ERR_UNSUPPORTED : DSMOE_ERR_INVALID, "down_em: bad shape (I a multiple of 256, <= 2048)");
+  if (block_m < 1 || block_m > kEmPairs) return fail(DSMOE_ERR_INVALID, "down_em: block_m must be in 1..8");
   if (pairs == 0) return DSMOE_OK;
   DnEmArgs m{};
   Shape sd;
@@ -635,13 +658,31 @@ int dsmoe_down_em(const void* down, const void* mq, const uint32_t* sorted_pairs
   m.tile_experts = tile_experts;
   m.tile_starts = tile_starts;
   m.tiles = (d + kDnEmRows - 1) / kDnEmRows;
-  const int64_t units = (int64_t)(pairs / kEmPairs + std::min(E, pairs)) * m.tiles;
+  m.np = block_m;
+  const int64_t units = (int64_t)(pairs / block_m + std::min(E, pairs)) * m.tiles;
   if (units > 0x7FFFFFFF) return fail(DSMOE_ERR_UNSUPPORTED, "down_em: too many pairs");
-  return launch(K_DN_EM, dim3((unsigned)units), dim3(256), down_em_lds(I / 256), stream, m);
+  return launch(K_DN_EM, dim3((unsigned)units), dim3(256), down_em_lds(I / 256, block_m), stream, m);
 }
 
-int dsmoe_q8_0_gemm(const void* w0, const void* w1, const uint16_t* xh, const float* xscale, float* out, int32_t in_dim,
-                    int32_t out_dim, int32_t T, float clamp, dsmoe_stream_t stream) {
+}  // extern "C"
+
+// Split over the row's lane classes for few token tiles: the smallest power
+// of two (<= 8, and a whole number of stages of 8 / jmax class positions)
+// that gives the launch at least `target` workgroups.
+static int q80_ksplit(int T, int in_dim, int out_dim, bool two) {
+  const int tiles = (T + kGuBM - 1) / kGuBM, ny = out_dim / (two ? 32 : 64);
+  const int jmax = (in_dim / 32 + 31) / 32, G = 8 / jmax;
+  int S = 1;
+  const int target = two ? 512 : 256;  // measured on c3 and c4 (the down GEMM has a quarter of the K)
+  while (S < 8 && (int64_t)tiles * ny * S < target && (32 / (2 * S)) % G == 0) S *= 2;
+  return S;
+}
+
+// The shared expert's GEMM; with `part` (at least ksplit * T * cols floats)
+// a split launch plus dsmoe_q80_combine when there are few token tiles.
+static int q80_gemm_impl(const void* w0, const void* w1, const uint16_t* xh, const float* xscale, float* out,
+                         int32_t in_dim, int32_t out_dim, int32_t T, float clamp, float* part, int32_t max_split,
+                         dsmoe_stream_t stream) {
   if (!w0 || !xh || !xscale || !out) return fail(DSMOE_ERR_INVALID, "q8_0_gemm: null pointer");
   if (!aligned16(w0) || (w1 && !aligned16(w1)) || !aligned16(xh))
     return fail(DSMOE_ERR_INVALID, "q8_0_gemm: weights and xh must be 16-byte aligned");
@@ -650,13 +691,26 @@ int dsmoe_q8_0_gemm(const void* w0, const void* w1, const uint16_t* xh, const fl
   if (((size_t)(in_dim / 32) * Q8_0_BYTES) % 4) return fail(DSMOE_ERR_UNSUPPORTED, "q8_0_gemm: rows must be 4-byte multiples");
   if (T == 0) return DSMOE_OK;
   Q80GemmArgs a{(const uint8_t*)w0, (const uint8_t*)w1, xh, xscale, out, in_dim, out_dim, T, clamp};
+  a.ksplit = part ? std::min(max_split, q80_ksplit(T, in_dim, out_dim, w1 != nullptr)) : 1;
+  a.part = a.ksplit > 1 ? part : nullptr;
   // kernels specialised on the blocks per lane class, ceil(in_dim / 1024)
   const int jmax = (in_dim / 32 + 31) / 32;
   const Kern kern = jmax == 7 ? (w1 ? K_Q80_GEMM_SWIGLU_J7 : K_Q80_GEMM_J7)
                   : jmax == 2 ? (w1 ? K_Q80_GEMM_SWIGLU_J2 : K_Q80_GEMM_J2)
                               : (w1 ? K_Q80_GEMM_SWIGLU : K_Q80_GEMM);
-  return launch(kern, dim3(xcd_grid((T + kGuBM - 1) / kGuBM, out_dim / (w1 ? 32 : 64))),
-                dim3(256), 0, stream, a);
+  DSM_TRY(launch(kern, dim3(xcd_grid((T + kGuBM - 1) / kGuBM, out_dim / (w1 ? 32 : 64) * a.ksplit)), dim3(256), 0,
+                 stream, a));
+  if (a.ksplit == 1) return DSMOE_OK;
+  Q80CombineArgs c{part, out, out_dim, T, a.ksplit, w1 ? 1 : 0, clamp};
+  const int64_t n = (int64_t)T * out_dim;
+  return launch(K_Q80_COMBINE, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, c);
+}
+
+extern "C" {
+
+int dsmoe_q8_0_gemm(const void* w0, const void* w1, const uint16_t* xh, const float* xscale, float* out, int32_t in_dim,
+                    int32_t out_dim, int32_t T, float clamp, dsmoe_stream_t stream) {
+  return q80_gemm_impl(w0, w1, xh, xscale, out, in_dim, out_dim, T, clamp, nullptr, 1, stream);
 }
 
 // --------------------------------------------------------------------------
@@ -694,6 +748,7 @@ struct dsmoe_ctx {
   uint32_t* g_tile_offsets = nullptr;
   uint32_t* g_tile_experts = nullptr;
   uint32_t* g_tile_starts = nullptr;
+  float* q80_part = nullptr;     // split shared-expert GEMM partials, [kQ80MaxSplit][min(T, 256)][cols]
   // mid row counters of the fused mid quantization in dsmoe_up_rows:
   // [kMaxDecodeT*k*(I/256)] routed, then [kMaxDecodeT*ceil(I_s/256)] shared;
   // zero between launches (the workgroup completing a block resets its word)
@@ -844,7 +899,7 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
     if (hipMemset(base, 0, nbytes) != hipSuccess) rc = fail(DSMOE_ERR_HIP, "create: hipMemset of the scratch failed");
   }
   if (max_tokens > kDecodeMaxT && E <= 512) {
-    const size_t P = T * K, max_tiles = P / std::min<size_t>(kGuBM, kEmPairs) + std::min(E, P);
+    const size_t P = T * K, max_tiles = P + std::min(E, P);  // dispatch tiles of any block_m >= 1
     A(&c->xh, T * d * 2);
     A(&c->mh, P * I * 2);
     A(&c->xh80, T * d * 2);
@@ -856,6 +911,7 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
     A(&c->g_tile_offsets, (E + 1) * 4);
     A(&c->g_tile_experts, max_tiles * 4);
     A(&c->g_tile_starts, max_tiles * 4);
+    A(&c->q80_part, (size_t)kQ80MaxSplit * std::min<size_t>(T, 256) * std::max<size_t>(2 * Is, d) * 4);
   }
   if (rc != DSMOE_OK) {
     std::string msg = g_err;
@@ -900,8 +956,8 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // runs the matvec launches, one work item per (row tile, pair / token).
   const bool grouped = T > kDecodeMaxT && c->xh != nullptr;
   // Few pairs per expert (at most kEmMaxLoad on average): the routed experts
-  // stream their weights once per chunk of kEmPairs pairs (expert-major
-  // matvec) instead of dequantizing them into MFMA tiles.
+  // stream their weights once per chunk of em_pairs() pairs
+  // (expert-major matvec) instead of dequantizing them into MFMA tiles.
   const bool em = grouped && (int64_t)P <= (int64_t)kEmMaxLoad * E && em_fits(cf);
   // 1. router logits + Q8_K(x) + Q8_0(x)          (session.rs:1894-1909, 1991-2008, 2062-2073)
   {
@@ -920,7 +976,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     StageScope sc(c, DSMOE_STAGE_SELECT, stream);
     DSM_TRY(dsmoe_router_select(&cf, c->logits, w->bias, T, nullptr, sel, wts, stream));
     if (grouped)  // moe_count/prefix/scatter_sorted_pairs + tiles (moe.rs:299-362, 547-596)
-      DSM_TRY(dsmoe_dispatch(sel, P, E, em ? kEmPairs : kGuBM, c->g_counts, c->g_offsets, c->g_sorted,
+      DSM_TRY(dsmoe_dispatch(sel, P, E, em ? em_pairs() : kGuBM, c->g_counts, c->g_offsets, c->g_sorted,
                              c->g_tile_offsets, c->g_tile_experts, c->g_tile_starts, stream));
   }
   // 3. routed + shared gate/up/SwiGLU              (session.rs:1910-1959, 2075-2112)
@@ -948,7 +1004,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
       StageScope sg(c, DSMOE_STAGE_GU_GROUPED, stream);
       DSM_TRY(dsmoe_gate_up_mid_em(w->gate, w->up, c->xq8k, c->g_sorted, c->g_offsets, c->g_tile_offsets,
                                    c->g_tile_experts, c->g_tile_starts, wts, c->mid, d, I, K, E, P,
-                                   cf.swiglu_clamp, stream));
+                                   em_pairs(), cf.swiglu_clamp, stream));
     } else if (grouped) {
       StageScope sg(c, DSMOE_STAGE_GU_GROUPED, stream);
       DSM_TRY(dsmoe_gate_up_mid_sorted(w->gate, w->up, c->xh, c->xq8k, c->g_sorted, c->g_offsets, c->g_tile_offsets,
@@ -973,7 +1029,8 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     if (grouped && cf.shared_fmt == 0) {  // shared expert as a GEMM over the whole batch
       a.sh_work = 0;
       StageScope sg(c, DSMOE_STAGE_SH_UP, stream);
-      DSM_TRY(dsmoe_q8_0_gemm(w->sh_gate, w->sh_up, c->xh80, c->xs80, c->sh_mid, d, Is, T, cf.swiglu_clamp, stream));
+      DSM_TRY(q80_gemm_impl(w->sh_gate, w->sh_up, c->xh80, c->xs80, c->sh_mid, d, Is, T, cf.swiglu_clamp,
+                            T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, stream));
     }
     if (fuse_midq) {
       a.fuse_midq = 1;
@@ -1008,7 +1065,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
         StageScope sg(c, DSMOE_STAGE_DN_GROUPED, stream);
         if (em) {
           DSM_TRY(dsmoe_down_em(w->down, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets, c->g_tile_experts,
-                                c->g_tile_starts, c->down_out, d, I, E, P, stream));
+                                c->g_tile_starts, c->down_out, d, I, E, P, em_pairs(), stream));
         } else {
           DSM_TRY(dsmoe_down_sorted(w->down, c->mh, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets,
                                     c->g_tile_experts, c->g_tile_starts, c->down_out, d, I, E, P, stream));
@@ -1030,7 +1087,8 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     if (grouped && cf.shared_fmt == 0) {
       a.sh_work = 0;
       StageScope sg(c, DSMOE_STAGE_SH_DN, stream);
-      DSM_TRY(dsmoe_q8_0_gemm(w->sh_down, nullptr, c->shh, c->sh_s80, shared_out, Is, d, T, 0.0f, stream));
+      DSM_TRY(q80_gemm_impl(w->sh_down, nullptr, c->shh, c->sh_s80, shared_out, Is, d, T, 0.0f,
+                            T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, stream));
     }
     if (rows) {
       a.dn_tiles = (d + kDnRowsR - 1) / kDnRowsR;

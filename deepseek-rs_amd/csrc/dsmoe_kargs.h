@@ -149,7 +149,7 @@ struct DnArgs {
 // pairs sorted by expert and cut into chunks of at most kEmPairs pairs of one
 // expert (dsmoe_dispatch with block_m = kEmPairs); grid = max chunks x tiles.
 constexpr int32_t kEmPairs = 8;  // DSMOE_EM_TILE_M
-constexpr int32_t kDnEmRows = 64;  // down rows per expert-major workgroup (8 per step)
+constexpr int32_t kDnEmRows = 128;  // down rows per expert-major workgroup (32 per step)
 struct GuEmArgs {
   GateUpArgs gu;  // selected unused; weights per pair; mid_out [pairs][I]
   const uint32_t* sorted_pairs;
@@ -158,6 +158,7 @@ struct GuEmArgs {
   const uint32_t* tile_experts;
   const uint32_t* tile_starts;
   int32_t tiles;                 // row tiles of 32 rows
+  int32_t np;                    // the dispatch's block_m (pairs per chunk), 1..kEmPairs
 };
 struct DnEmArgs {
   DownArgs dn;    // selected and out unused; down_out [pairs][d]
@@ -167,6 +168,7 @@ struct DnEmArgs {
   const uint32_t* tile_experts;
   const uint32_t* tile_starts;
   int32_t tiles;                 // row tiles of kDnEmRows rows
+  int32_t np;                    // the dispatch's block_m (pairs per chunk), 1..kEmPairs
 };
 
 // Largest token count of the row-streaming (decode) launches.
@@ -219,6 +221,21 @@ struct Q80GemmArgs {
   const float* xs;        // activation block scales [T][in_dim/32]
   float* out;             // [T][out_dim]: swiglu(gate, up) (weight 1), or the product
   int32_t in_dim, out_dim, T;
+  float clamp;
+  // split over the row's 32 lane classes (few token tiles): workgroup s of a
+  // slab sums class positions [s * 32 / ksplit, (s + 1) * 32 / ksplit) into
+  // part[s][T][cols] (cols = out_dim, gate then up columns with w1), and
+  // dsmoe_q80_combine finishes the tree; ksplit = 1 writes out directly
+  float* part = nullptr;
+  int32_t ksplit = 1;
+};
+// dsmoe_q80_combine: out[t][c] from the ksplit partial sums (pairwise in
+// split order, the top levels of the row's halving tree), then SwiGLU when
+// the GEMM had two matrices.
+struct Q80CombineArgs {
+  const float* part;  // [ksplit][T][cols]
+  float* out;         // [T][out_dim]
+  int32_t out_dim, T, ksplit, two;
   float clamp;
 };
 

@@ -989,18 +989,20 @@ __device__ __forceinline__ void role_gate_up_rows(const GateUpArgs& a, int tile,
 // ---------------------------------------------------------------------------
 // Expert-major gate/up/SwiGLU (batches with few pairs per expert; the
 // reference's moe_gate_up_mid_sorted_qwarp32, moe.rs:721-815, per-pair
-// arithmetic of :622-715).  A workgroup takes one chunk of up to kEmPairs
-// pairs of one expert (a dsmoe_dispatch tile with block_m = kEmPairs) and 32
-// rows of gate and of up: the weight rows stream once, in the row-streaming
-// layout above (4 lanes per row, lane j takes blocks j, j+4, ...), and every
-// decoded block is multiplied with the activations of all the chunk's pairs,
-// staged in LDS.  The signs go onto the grid bytes before the products
-// (exact: every signed grid byte is in [-43, 43]), so a pair costs two
-// dot4 per 8 weights.  Each pair's sum keeps the reference's order (block
-// classes j and j+4 in-lane, then xor 2, xor 1), so the bits equal the
-// per-pair kernels'.
-// LDS (all dynamic): tables | q8[kEmPairs][nb][272] (each block's d in
-// bytes 256..259 of its padding); the row sums reuse the q8 space after the
+// arithmetic of :622-715).  A workgroup takes one chunk of up to m.np pairs
+// of one expert (a dsmoe_dispatch tile with block_m = m.np <= kEmPairs) and
+// 32 rows of gate and of up: the weight rows stream once, in the
+// row-streaming layout above (4 lanes per row, lane j takes blocks j, j+4,
+// ...), and every decoded block is multiplied with the activations of the
+// chunk's pairs, staged in LDS (the pair loop runs the chunk's count; a
+// branch-free loop over a compiled count let the compiler hoist every
+// lookup and spill).  The signs go onto the
+// grid bytes before the products (exact: every signed grid byte is in
+// [-43, 43]), so a pair costs two dot4 per 8 weights.  Each pair's sum keeps
+// the reference's order (block classes j and j+4 in-lane, then xor 2, xor
+// 1), so the bits equal the per-pair kernels'.
+// LDS (all dynamic): tables | q8[m.np][nb][272] (each block's d in bytes
+// 256..259 of its padding); the row sums reuse the q8 space after the
 // products.
 // ---------------------------------------------------------------------------
 
@@ -1013,16 +1015,13 @@ __device__ __forceinline__ uint32_t signed_grid4(uint32_t g, uint32_t m) {
 }
 
 template <int kNit>
-__device__ __forceinline__ void role_gate_up_em(const GuEmArgs& m, int tile, int chunk, uint8_t* smem) {
+__device__ __forceinline__ void role_gate_up_em(const GuEmArgs& m, int tile, int e, int p0, int cnt, uint8_t* smem) {
+  constexpr int NP = kEmPairs;
   const GateUpArgs& a = m.gu;
   const int nb = a.d >> 8, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
-  if (chunk >= (int)m.tile_offsets[a.E]) return;
-  const int e = (int)m.tile_experts[chunk];
-  const int p0 = (int)(m.offsets[e] + m.tile_starts[chunk]);
-  const int cnt = min(kEmPairs, (int)m.offsets[e + 1] - p0);
   Iq2Tables* tab = (Iq2Tables*)smem;
-  uint8_t* s_q8 = smem + sizeof(Iq2Tables);  // [kEmPairs][nb][272]
-  float* s_rows = (float*)s_q8;              // [kEmPairs][64], after the products
+  uint8_t* s_q8 = smem + sizeof(Iq2Tables);  // [np][nb][272]
+  float* s_rows = (float*)s_q8;              // [NP][64], after the products
 
   const int row0 = tile * 32, mat = wv >> 1, rr = (wv & 1) * 16 + (lane >> 2), j = lane & 3;
   const int row = min(row0 + rr, a.I - 1);
@@ -1034,32 +1033,44 @@ __device__ __forceinline__ void role_gate_up_em(const GuEmArgs& m, int tile, int
   for (int i = 0; i < 3 && i < kNit; i++) DSM_BLK_LOAD(wb[i], i)
   if (tid < 128) tab->mask[tid] = sign_mask64(iq2_sign_byte(tid));
   tab->grid[tid & 255] = kIq2xxsGrid[tid & 255];
-  // activations of the chunk's pairs: per pair nb * 64 qs words then nb d words
+  // activations of the chunk's pairs: per pair nb * 64 qs words then nb d
+  // words, eight independent loads in flight per thread before their stores
   const int per = nb * 65;
-  for (int i = tid; i < cnt * per; i += 256) {
-    const int jj = i / per, r = i - jj * per;
-    const uint32_t pair = m.sorted_pairs[p0 + jj];
-    const uint8_t* src = a.xq + (size_t)(pair / (uint32_t)a.k) * nb * Q8K_BYTES;
-    if (r < nb * 64) {
-      *(uint32_t*)(s_q8 + ((size_t)jj * nb + (r >> 6)) * kQ8Stride + 4 * (r & 63)) =
-          *(const uint32_t*)(src + (size_t)(r >> 6) * Q8K_BYTES + 4 + 4 * (r & 63));
-    } else {
-      *(float*)(s_q8 + ((size_t)jj * nb + (r - nb * 64)) * kQ8Stride + 256) = ld_f32(src + (size_t)(r - nb * 64) * Q8K_BYTES);
+#pragma unroll
+  for (int q = 0; q < NP; q++) {
+    if (q < cnt) {
+      const uint8_t* src = a.xq + (size_t)(m.sorted_pairs[p0 + q] / (uint32_t)a.k) * nb * Q8K_BYTES;
+      uint8_t* dst = s_q8 + (size_t)q * nb * kQ8Stride;
+      for (int i0 = 0; i0 < per; i0 += 8 * 256) {
+        uint32_t v[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          const int r = min(i0 + t * 256 + tid, per - 1);
+          v[t] = r < nb * 64 ? *(const uint32_t*)(src + (size_t)(r >> 6) * Q8K_BYTES + 4 + 4 * (r & 63))
+                             : *(const uint32_t*)(src + (size_t)(r - nb * 64) * Q8K_BYTES);
+        }
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          const int r = i0 + t * 256 + tid;
+          if (r < nb * 64) *(uint32_t*)(dst + (r >> 6) * kQ8Stride + 4 * (r & 63)) = v[t];
+          else if (r < per) *(uint32_t*)(dst + (r - nb * 64) * kQ8Stride + 256) = v[t];
+        }
+      }
     }
   }
   __syncthreads();
 
-  float p_lo[kEmPairs], p_hi[kEmPairs];
+  float p_lo[NP], p_hi[NP];
 #pragma unroll
-  for (int q = 0; q < kEmPairs; q++) { p_lo[q] = 0.0f; p_hi[q] = 0.0f; }
+  for (int q = 0; q < NP; q++) { p_lo[q] = 0.0f; p_hi[q] = 0.0f; }
 #pragma unroll
   for (int i = 0; i < kNit; i++) {
     const int b = j + 4 * i;
     if (b < nb) {
       const uint32_t* w = wb[i % 3];
-      int32_t bsum[kEmPairs];
+      int32_t bsum[NP];
 #pragma unroll
-      for (int q = 0; q < kEmPairs; q++) bsum[q] = 0;
+      for (int q = 0; q < NP; q++) bsum[q] = 0;
 #pragma unroll
       for (int ib = 0; ib < 8; ib++) {
         const uint32_t aux0 = __builtin_amdgcn_perm(w[2 * ib + 1], w[2 * ib], sel);
@@ -1074,43 +1085,40 @@ __device__ __forceinline__ void role_gate_up_em(const GuEmArgs& m, int tile, int
         }
         const int32_t ls = (int32_t)((aux1 >> 27) | 1u);
 #pragma unroll
-        for (int q = 0; q < kEmPairs; q++) {
-          if (q < cnt) {
-            const uint8_t* q8 = s_q8 + ((size_t)q * nb + b) * kQ8Stride + ib * 32;
-            const uint4 qa = *(const uint4*)q8, qb = *(const uint4*)(q8 + 16);
-            int32_t sumi = dot4(sg[0], qa.x, 0);
-            sumi = dot4(sg[1], qa.y, sumi);
-            sumi = dot4(sg[2], qa.z, sumi);
-            sumi = dot4(sg[3], qa.w, sumi);
-            sumi = dot4(sg[4], qb.x, sumi);
-            sumi = dot4(sg[5], qb.y, sumi);
-            sumi = dot4(sg[6], qb.z, sumi);
-            sumi = dot4(sg[7], qb.w, sumi);
-            bsum[q] += __mul24(sumi, ls);  // |sumi| < 2^18, ls <= 31
-          }
+        for (int q = 0; q < NP; q++) {
+          if (q >= cnt) break;
+          const uint8_t* q8 = s_q8 + ((size_t)q * nb + b) * kQ8Stride + ib * 32;
+          const uint4 qa = *(const uint4*)q8, qb = *(const uint4*)(q8 + 16);
+          int32_t sumi = dot4(sg[0], qa.x, 0);
+          sumi = dot4(sg[1], qa.y, sumi);
+          sumi = dot4(sg[2], qa.z, sumi);
+          sumi = dot4(sg[3], qa.w, sumi);
+          sumi = dot4(sg[4], qb.x, sumi);
+          sumi = dot4(sg[5], qb.y, sumi);
+          sumi = dot4(sg[6], qb.z, sumi);
+          sumi = dot4(sg[7], qb.w, sumi);
+          bsum[q] += __mul24(sumi, ls);  // |sumi| < 2^18, ls <= 31
         }
       }
       const float xd = f16_to_f32_ftz((uint16_t)(w[0] >> dsh));
 #pragma unroll
-      for (int q = 0; q < kEmPairs; q++) {
-        if (q < cnt) {
-          const float yd = *(const float*)(s_q8 + ((size_t)q * nb + b) * kQ8Stride + 256);
-          const float v = 0.125f * xd * yd * (float)bsum[q];
-          if (i & 1) p_hi[q] += v; else p_lo[q] += v;
-        }
+      for (int q = 0; q < NP; q++) {
+        if (q >= cnt) break;
+        const float yd = *(const float*)(s_q8 + ((size_t)q * nb + b) * kQ8Stride + 256);
+        const float v = 0.125f * xd * yd * (float)bsum[q];
+        if (i & 1) p_hi[q] += v; else p_lo[q] += v;
       }
     }
     if (i + 3 < kNit) DSM_BLK_LOAD(wb[i % 3], i + 3)
   }
   __syncthreads();  // every wave is done with the staged activations
 #pragma unroll
-  for (int q = 0; q < kEmPairs; q++) {
-    if (q < cnt) {
-      float v = p_lo[q] + p_hi[q];   // halving tree, level xor 4 (in-lane)
-      v += __shfl_xor(v, 2, 64);     // level xor 2
-      v += __shfl_xor(v, 1, 64);     // level xor 1
-      if (j == 0) s_rows[q * 64 + mat * 32 + rr] = v;
-    }
+  for (int q = 0; q < NP; q++) {
+    if (q >= cnt) break;
+    float v = p_lo[q] + p_hi[q];   // halving tree, level xor 4 (in-lane)
+    v += __shfl_xor(v, 2, 64);     // level xor 2
+    v += __shfl_xor(v, 1, 64);     // level xor 1
+    if (j == 0) s_rows[q * 64 + mat * 32 + rr] = v;
   }
   __syncthreads();
   for (int i = tid; i < cnt * 32; i += 256) {
@@ -1284,66 +1292,71 @@ __device__ __forceinline__ void role_down_rows_any(const DownArgs& a, int tile, 
 
 // Expert-major down projection (batches with few pairs per expert;
 // moe_down_sorted_qwarp32, moe.rs:871-916): a workgroup takes one chunk of
-// up to kEmPairs (8) pairs of one expert and kDnEmRows rows of its down
-// matrix, 8 rows per step (2 per wave), the next step's weights in flight
-// during the current one.  Lane l takes pair l/8 of the chunk and block
-// l mod 8 of the row (the reference's lane-strided partial), so the 8 lanes
-// of a block read the same weight bytes; the 8-lane butterfly finishes each
-// pair's row and the value goes to down_out[pair][row] (the slot-ordered sum
-// runs after, in dsmoe_moe_sum).  I <= 2048 (one block per lane).
-// LDS: yd[kEmPairs*nb] | bsums[kEmPairs*nb][16] | q8[kEmPairs*nb][272]
+// up to kEmPairs pairs of one expert and kDnEmRows rows of its down matrix,
+// 32 rows per step (8 per wave), the next step's weights in flight during
+// the current one.  Lane l of a wave takes row l/8 of the wave's eight and
+// block l mod 8 of it (the reference's lane-strided partial), holds that
+// block in registers and runs it against every pair of the chunk; the
+// 8-lane butterfly finishes each pair's row and the value goes to
+// down_out[pair][row] (the slot-ordered sum runs after, in dsmoe_moe_sum).
+// I <= 2048 (one block per lane).
+// LDS: the chunk's Q8_K(mid) blocks as copied, [kEmPairs][nb] slots of 304
+// bytes starting at byte 12 of a slot (the 256 qs bytes 16-byte aligned).
 __device__ __forceinline__ void role_down_em(const DnEmArgs& m, int tile, int chunk, uint8_t* smem) {
   const DownArgs& a = m.dn;
   const int nb = a.I >> 8, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
   if (chunk >= (int)m.tile_offsets[a.E]) return;
   const int e = (int)m.tile_experts[chunk];
   const int p0 = (int)(m.offsets[e] + m.tile_starts[chunk]);
-  const int cnt = min(kEmPairs, (int)m.offsets[e + 1] - p0);
-  float* s_yd = (float*)smem;
-  int16_t* s_bs = (int16_t*)(s_yd + align_up(kEmPairs * nb, 4));
-  uint8_t* s_q8 = (uint8_t*)(s_bs + kEmPairs * nb * 16);
-  const int q = lane >> 3, j = lane & 7;
-  constexpr int kSteps = kDnEmRows / 8;
+  const int cnt = min(m.np, (int)m.offsets[e + 1] - p0);
+  constexpr int kSlot = 304, kSteps = kDnEmRows / 32;
+  const int rl = lane >> 3, j = lane & 7;
   const size_t row_bytes = (size_t)nb * Q2K_BYTES;
-  const int row0 = tile * kDnEmRows;
+  const int row0 = tile * kDnEmRows + wv * 8 + rl;
   const uint8_t* wbase = a.down + (size_t)e * a.d * row_bytes + (size_t)min(j, nb - 1) * Q2K_BYTES;
-  auto load = [&](int st, uint32_t (&w)[2][21]) {
+  auto load = [&](int st, uint32_t (&w)[21]) {
+    const uint8_t* src = wbase + (size_t)min(row0 + 32 * st, a.d - 1) * row_bytes;
 #pragma unroll
-    for (int r = 0; r < 2; r++) {
-      const int row = min(row0 + 8 * st + wv + 4 * r, a.d - 1);
-      const uint8_t* src = wbase + (size_t)row * row_bytes;
-#pragma unroll
-      for (int c = 0; c < 5; c++) {
-        const uint4 v4 = *(const uint4*)(src + 16 * c);
-        w[r][4 * c] = v4.x; w[r][4 * c + 1] = v4.y; w[r][4 * c + 2] = v4.z; w[r][4 * c + 3] = v4.w;
-      }
-      w[r][20] = *(const uint32_t*)(src + 80);
+    for (int c = 0; c < 5; c++) {
+      const uint4 v4 = *(const uint4*)(src + 16 * c);
+      w[4 * c] = v4.x; w[4 * c + 1] = v4.y; w[4 * c + 2] = v4.z; w[4 * c + 3] = v4.w;
     }
+    w[20] = *(const uint32_t*)(src + 80);
   };
-  uint32_t wa[2][21], wb[2][21];
+  uint32_t wa[21], wb[21];
   load(0, wa);
-  // the chunk's Q8_K(mid) blocks: per block 64 qs words, 1 d word, 8 bsums words
-  const int nblk = cnt * nb;
-  for (int i = tid; i < nblk * 73; i += 256) {
-    const int blk = i / 73, r = i - blk * 73, qq = blk / nb, b = blk - qq * nb;
-    const uint32_t pair = m.sorted_pairs[p0 + qq];
-    const uint8_t* src = a.midq + ((size_t)pair * nb + b) * Q8K_BYTES;
-    if (r < 64) *(uint32_t*)(s_q8 + (size_t)blk * kQ8Stride + 4 * r) = *(const uint32_t*)(src + 4 + 4 * r);
-    else if (r == 64) s_yd[blk] = ld_f32(src);
-    else ((uint32_t*)s_bs)[blk * 8 + (r - 65)] = *(const uint32_t*)(src + 260 + 4 * (r - 65));
+  // the chunk's Q8_K(mid) blocks, 73 words each, copied whole
+  const int per = nb * 73;
+#pragma unroll
+  for (int q = 0; q < kEmPairs; q++) {
+    if (q < cnt) {
+      const uint32_t* src = (const uint32_t*)(a.midq + (size_t)m.sorted_pairs[p0 + q] * nb * Q8K_BYTES);
+      uint8_t* dst = smem + (size_t)q * nb * kSlot + 12;
+      for (int i0 = 0; i0 < per; i0 += 4 * 256) {
+        uint32_t v[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) v[t] = src[min(i0 + t * 256 + tid, per - 1)];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const int r = i0 + t * 256 + tid;
+          if (r < per) *(uint32_t*)(dst + (r / 73) * kSlot + 4 * (r % 73)) = v[t];
+        }
+      }
+    }
   }
   __syncthreads();
-  const bool live = q < cnt && j < nb;
-  const int qb = q * nb + j;
-  const uint32_t pair = m.sorted_pairs[p0 + min(q, cnt - 1)];
-  auto run = [&](int st, const uint32_t (&w)[2][21]) {
+  const uint8_t* slot0 = smem + (size_t)min(j, nb - 1) * kSlot + 12;
+  auto run = [&](int st, const uint32_t (&w)[21]) {
+    const int row = row0 + 32 * st;
 #pragma unroll
-    for (int r = 0; r < 2; r++) {
-      float p = 0.0f;  // the reference's lane-strided partial j of this pair's row
-      if (live) p = q2k_block_dot(w[r], s_q8 + qb * kQ8Stride, s_bs + qb * 16, s_yd[qb]);
-      p = group_sum<8>(p);
-      const int row = row0 + 8 * st + wv + 4 * r;
-      if (j == 0 && q < cnt && row < a.d) a.down_out[(size_t)pair * a.d + row] = p;
+    for (int q = 0; q < kEmPairs; q++) {
+      if (q < cnt) {
+        const uint8_t* blk = slot0 + (size_t)q * nb * kSlot;
+        // the reference's lane-strided partial j of this pair's row
+        float p = j < nb ? q2k_block_dot(w, blk + 4, (const int16_t*)(blk + 260), *(const float*)blk) : 0.0f;
+        p = group_sum<8>(p);
+        if (j == 0 && row < a.d) a.down_out[(size_t)m.sorted_pairs[p0 + q] * a.d + row] = p;
+      }
     }
   };
 #pragma unroll
@@ -1992,15 +2005,19 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_dn_rows(const DnArgs a) 
 extern "C" __global__ __launch_bounds__(256) void dsmoe_up_em(const GuEmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int tile = blockIdx.x % a.tiles, chunk = blockIdx.x / a.tiles;
+  if (chunk >= (int)a.tile_offsets[a.gu.E]) return;
+  const int e = (int)a.tile_experts[chunk];
+  const int p0 = (int)(a.offsets[e] + a.tile_starts[chunk]);
+  const int cnt = min(a.np, (int)a.offsets[e + 1] - p0);
   switch ((a.gu.d + 1023) >> 10) {  // blocks per lane (d <= 8192)
-    case 1: role_gate_up_em<1>(a, tile, chunk, smem); break;
-    case 2: role_gate_up_em<2>(a, tile, chunk, smem); break;
-    case 3: role_gate_up_em<3>(a, tile, chunk, smem); break;
-    case 4: role_gate_up_em<4>(a, tile, chunk, smem); break;
-    case 5: role_gate_up_em<5>(a, tile, chunk, smem); break;
-    case 6: role_gate_up_em<6>(a, tile, chunk, smem); break;
-    case 7: role_gate_up_em<7>(a, tile, chunk, smem); break;
-    default: role_gate_up_em<8>(a, tile, chunk, smem); break;
+    case 1: role_gate_up_em<1>(a, tile, e, p0, cnt, smem); break;
+    case 2: role_gate_up_em<2>(a, tile, e, p0, cnt, smem); break;
+    case 3: role_gate_up_em<3>(a, tile, e, p0, cnt, smem); break;
+    case 4: role_gate_up_em<4>(a, tile, e, p0, cnt, smem); break;
+    case 5: role_gate_up_em<5>(a, tile, e, p0, cnt, smem); break;
+    case 6: role_gate_up_em<6>(a, tile, e, p0, cnt, smem); break;
+    case 7: role_gate_up_em<7>(a, tile, e, p0, cnt, smem); break;
+    default: role_gate_up_em<8>(a, tile, e, p0, cnt, smem); break;
   }
 }
 

@@ -74,8 +74,8 @@ def lib():
         "dsmoe_destroy": ([vp], i32),
         "dsmoe_scratch_bytes": ([vp], ctypes.c_size_t),
         "dsmoe_forward": ([vp, ctypes.POINTER(Weights), vp, i32, vp, vp, vp, vp, vp], i32),
-        "dsmoe_gate_up_mid_em": ([vp] * 10 + [i32, i32, i32, i32, i32, f32, vp], i32),
-        "dsmoe_down_em": ([vp] * 8 + [i32, i32, i32, i32, vp], i32),
+        "dsmoe_gate_up_mid_em": ([vp] * 10 + [i32, i32, i32, i32, i32, i32, f32, vp], i32),
+        "dsmoe_down_em": ([vp] * 8 + [i32, i32, i32, i32, i32, vp], i32),
         "dsmoe_probe": ([i32, vp, ctypes.c_size_t, ctypes.c_int64, vp, vp], i32),
         "dsmoe_hc_expand": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp], i32),
         "dsmoe_forward_noalloc": ([ctypes.POINTER(Config), ctypes.POINTER(Weights), vp, i32, vp, vp, vp, vp, vp], i32),
@@ -308,18 +308,18 @@ EM_TILE_M = 8
 
 
 def gate_up_mid_em(gate, up, xq, sorted_pairs, offsets, tile_offsets, tile_experts, tile_starts, weights, mid_out,
-                   d, I, k, E, pairs, clamp, stream=None):
-    """Expert-major gate/up/SwiGLU over pairs dispatched with block_m = EM_TILE_M (moe.rs:721-815)."""
+                   d, I, k, E, pairs, clamp, block_m=EM_TILE_M, stream=None):
+    """Expert-major gate/up/SwiGLU over pairs dispatched with block_m <= EM_TILE_M (moe.rs:721-815)."""
     check(lib().dsmoe_gate_up_mid_em(_p(gate), _p(up), _p(xq), _p(sorted_pairs), _p(offsets), _p(tile_offsets),
                                      _p(tile_experts), _p(tile_starts), _p(weights), _p(mid_out), d, I, k, E, pairs,
-                                     clamp, _stream(stream)))
+                                     block_m, clamp, _stream(stream)))
 
 
 def down_em(w, mq, sorted_pairs, offsets, tile_offsets, tile_experts, tile_starts, down_out, d, I, E, pairs,
-            stream=None):
-    """Expert-major down over pairs dispatched with block_m = EM_TILE_M (moe.rs:871-916)."""
+            block_m=EM_TILE_M, stream=None):
+    """Expert-major down over pairs dispatched with block_m <= EM_TILE_M (moe.rs:871-916)."""
     check(lib().dsmoe_down_em(_p(w), _p(mq), _p(sorted_pairs), _p(offsets), _p(tile_offsets), _p(tile_experts),
-                              _p(tile_starts), _p(down_out), d, I, E, pairs, _stream(stream)))
+                              _p(tile_starts), _p(down_out), d, I, E, pairs, block_m, _stream(stream)))
 
 
 def probe(kind, src, nbytes, iters, sink, stream=None):

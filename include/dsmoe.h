@@ -201,23 +201,25 @@ int dsmoe_gate_up_mid_sorted(const void* gate, const void* up, const uint16_t* x
 
 /* moe_gate_up_mid_sorted_qwarp32 (engine/src/kernels/moe.rs:721-815) in
  * the expert-major matvec form, for batches with few pairs per expert: the
- * pairs grouped by dsmoe_dispatch with block_m = DSMOE_EM_TILE_M; every
- * expert's weight rows stream once per tile of up to 8 pairs, each decoded
- * block multiplied with all the tile's activations.  xq: Q8_K(x).  Same bits
- * as dsmoe_gate_up_mid.  d a multiple of 512, at most 7168. */
+ * pairs grouped by dsmoe_dispatch with block_m (1..DSMOE_EM_TILE_M); every
+ * expert's weight rows stream once per tile of up to block_m pairs, each
+ * decoded block multiplied with all the tile's activations.  xq: Q8_K(x).
+ * Same bits as dsmoe_gate_up_mid.  d a multiple of 512 whose block_m
+ * activations fit the workgroup's LDS (block_m 8: d <= 7168). */
 #define DSMOE_EM_TILE_M 8
 int dsmoe_gate_up_mid_em(const void* gate, const void* up, const void* xq, const uint32_t* sorted_pairs,
                          const uint32_t* offsets, const uint32_t* tile_offsets, const uint32_t* tile_experts,
                          const uint32_t* tile_starts, const float* weights, float* mid_out, int32_t d, int32_t I,
-                         int32_t k, int32_t E, int32_t pairs, float clamp, dsmoe_stream_t stream);
+                         int32_t k, int32_t E, int32_t pairs, int32_t block_m, float clamp, dsmoe_stream_t stream);
 
 /* moe_down_sorted_qwarp32 (moe.rs:871-916) in the expert-major form:
- * down_out[pair][row] for the pairs grouped by dsmoe_dispatch with block_m =
- * DSMOE_EM_TILE_M; mq: Q8_K(mid).  Same bits as dsmoe_down's per-pair
+ * down_out[pair][row] for the pairs grouped by dsmoe_dispatch with block_m
+ * (1..DSMOE_EM_TILE_M); mq: Q8_K(mid).  Same bits as dsmoe_down's per-pair
  * values; the slot sum is dsmoe_moe_sum.  I at most 2048. */
 int dsmoe_down_em(const void* down, const void* mq, const uint32_t* sorted_pairs, const uint32_t* offsets,
                   const uint32_t* tile_offsets, const uint32_t* tile_experts, const uint32_t* tile_starts,
-                  float* down_out, int32_t d, int32_t I, int32_t E, int32_t pairs, dsmoe_stream_t stream);
+                  float* down_out, int32_t d, int32_t I, int32_t E, int32_t pairs, int32_t block_m,
+                  dsmoe_stream_t stream);
 
 /* moe_down_sorted_qwarp32 (engine/src/kernels/moe.rs:821-916, sorted
  * variant): down_out[pair][row] for the pairs grouped by dsmoe_dispatch

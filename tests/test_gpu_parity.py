@@ -299,14 +299,15 @@ def test_gate_up_sorted_matches_per_pair(gpu, d, I, E, T, k, skew, big):
     assert bits_equal(np_(dd), np_(dd_ref))
 
 
-@pytest.mark.parametrize("d,I,E,T,k,skew", [(7168, 2048, 16, 40, 8, True), (7168, 2048, 256, 32, 8, False),
-                                             (2048, 1536, 8, 5, 3, False), (1024, 512, 3, 9, 2, True)])
-def test_expert_major_matches_per_pair(gpu, d, I, E, T, k, skew):
+@pytest.mark.parametrize("d,I,E,T,k,skew,bm", [(7168, 2048, 16, 40, 8, True, 8), (7168, 2048, 256, 32, 8, False, 2),
+                                                (7168, 2048, 64, 32, 8, True, 4), (2048, 1536, 8, 5, 3, False, 8),
+                                                (1024, 512, 3, 9, 2, True, 3)])
+def test_expert_major_matches_per_pair(gpu, d, I, E, T, k, skew, bm):
     """The expert-major gate/up and down (pairs dispatched in tiles of 8, each
     expert's rows streamed once per tile) must give the per-pair kernels'
     bits: hot experts with several tiles, cold ones with one pair."""
     import torch
-    say(f"expert-major d={d} I={I} E={E} T={T} k={k} skew={skew}")
+    say(f"expert-major d={d} I={I} E={E} T={T} k={k} skew={skew} block_m={bm}")
     rng = np.random.default_rng(d + I + T + 1)
     gate = dsmoe.synth(dsmoe.FMT_IQ2_XXS, 4, 1, E, I, d, sigma=0.02, device=gpu)
     up = dsmoe.synth(dsmoe.FMT_IQ2_XXS, 4, 2, E, I, d, sigma=0.02, device=gpu)
@@ -329,11 +330,11 @@ def test_expert_major_matches_per_pair(gpu, d, I, E, T, k, skew):
     u32 = dict(dtype=torch.int32, device=gpu)
     counts, offsets = torch.empty(E, **u32), torch.empty(E + 1, **u32)
     sp = torch.empty(P_, **u32)
-    max_tiles = P_ // dsmoe.EM_TILE_M + min(E, P_)
+    max_tiles = P_ // bm + min(E, P_)
     toff, texp, tst = torch.empty(E + 1, **u32), torch.empty(max_tiles, **u32), torch.empty(max_tiles, **u32)
-    dsmoe.dispatch(dsel, P_, E, dsmoe.EM_TILE_M, counts, offsets, sp, toff, texp, tst)
+    dsmoe.dispatch(dsel, P_, E, bm, counts, offsets, sp, toff, texp, tst)
     m = torch.full((P_, I), float("nan"), device=gpu)
-    dsmoe.gate_up_mid_em(gate, up, xq, sp, offsets, toff, texp, tst, dw, m, d, I, k, E, P_, 10.0)
+    dsmoe.gate_up_mid_em(gate, up, xq, sp, offsets, toff, texp, tst, dw, m, d, I, k, E, P_, 10.0, bm)
     torch.cuda.synchronize()
     say(f"  tiles={int(np_(toff)[-1])} max_count={int(np_(counts).max())}")
     assert_close(np_(m).reshape(-1), np_(m_ref).reshape(-1), "mid expert-major vs per-pair")
@@ -343,7 +344,7 @@ def test_expert_major_matches_per_pair(gpu, d, I, E, T, k, skew):
     dd_ref = torch.empty(P_, d, device=gpu)
     dsmoe.down(dn, mq, dsel, dd_ref, None, d, I, T, k, E)
     dd = torch.full((P_, d), float("nan"), device=gpu)
-    dsmoe.down_em(dn, mq, sp, offsets, toff, texp, tst, dd, d, I, E, P_)
+    dsmoe.down_em(dn, mq, sp, offsets, toff, texp, tst, dd, d, I, E, P_, bm)
     torch.cuda.synchronize()
     assert_close(np_(dd).reshape(-1), np_(dd_ref).reshape(-1), "down expert-major vs per-pair")
     assert bits_equal(np_(dd), np_(dd_ref))
