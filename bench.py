@@ -125,15 +125,14 @@ STAGE_KERNEL = {"prep": "dsmoe_prep", "select": "dsmoe_router_select", "up": "ds
 
 def code_object_hash(kernel):
     """First 16 hex digits of the SHA-256 of the code object holding `kernel`
-    (dsmoe_gemm.hsaco for the grouped GEMMs and the batch router, else
-    dsmoe_kernels.hsaco)."""
-    import hashlib
-    lib = os.path.join(ROOT, "deepseek-rs_amd", "lib")
-    gemm = kernel.startswith(("dsmoe_gu_grouped", "dsmoe_dn_grouped", "dsmoe_q80_gemm", "dsmoe_router_tile"))
-    f = os.path.join(lib, "dsmoe_gemm.hsaco" if gemm else "dsmoe_kernels.hsaco")
-    if not os.path.exists(f):
-        return None
-    return hashlib.sha256(open(f, "rb").read()).hexdigest()[:16]
+    (deepseek-rs_amd/profile_summary.py, which stamps the same hash on every
+    profile line)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("dsmoe_profile_summary",
+                                                  os.path.join(ROOT, "deepseek-rs_amd", "profile_summary.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.code_object_hash(kernel)
 
 
 def measured_traffic(kernel, config, path, profiles=None):
@@ -161,29 +160,121 @@ def layer_bytes(cfg, n_distinct):
     return n_distinct * cfg.bytes_per_expert() + cfg.bytes_shared() + cfg.bytes_router()
 
 
-def cpu_baseline(case, w, xs, seconds, cores):
+def box_peaks(dev):
+    """What this GPU sustains with no algorithm around it (dsmoe_probe):
+    dense f16 MFMA TFLOP/s and HBM read GB/s, reported next to the
+    published peaks the roofline fractions use."""
+    import torch
+    import dsmoe
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.zeros(8 * cus, device=dev)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    iters = 4096
+    dsmoe.probe(0, None, 0, 64, sink)
+    torch.cuda.synchronize()
+    a.record()
+    dsmoe.probe(0, None, 0, iters, sink)
+    b.record()
+    torch.cuda.synchronize()
+    waves = 2 * cus * 4
+    mfma = waves * iters * 8 * 32768 / (a.elapsed_time(b) * 1e-3) / 1e12
+    buf = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
+    dsmoe.probe(1, buf, buf.numel(), 0, sink)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(5):
+        dsmoe.probe(1, buf, buf.numel(), 0, sink)
+    b.record()
+    torch.cuda.synchronize()
+    hbm = 5 * buf.numel() / (a.elapsed_time(b) * 1e-3) / 1e9
+    del buf
+    return {"mfma_f16_dense_TFLOPs": round(mfma, 1), "hbm_read_GBps": round(hbm, 1), "cus": cus,
+            "note": "dsmoe_probe: 8 independent v_mfma_f32_32x32x16_f16 chains per wave, 2 waves per SIMD; "
+                    "one 2 GiB read with 16-byte nontemporal loads"}
+
+
+def host_info():
+    model = "?"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model}
+
+
+def config_bench(case, w, steps, warmup, dev):
+    """Tokens/s of one more config on the same library path, with the
+    layer's algorithmic HBM bytes (router, the distinct experts' weights,
+    shared expert) and, for the grouped path, its MFMA flops."""
+    import numpy as np
+    import torch
+    import dsmoe
+    from dsmoe import configs as C
+    cfg, T = case.cfg, case.T
+    xs = [C.make_x(case, T=T, step=s, device=dev) for s in range(4)]
+    layer = dsmoe.MoeLayer(cfg, T)
+    d, k = cfg.d_model, cfg.top_k
+    so, ro = torch.empty(T, d, device=dev), torch.empty(T, d, device=dev)
+    sel = torch.empty(T, k, dtype=torch.int32, device=dev)
+    wt = torch.empty(T, k, device=dev)
+    step = lambda i: layer.forward(w, xs[i % len(xs)], so, ro, sel, wt)
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(steps):
+        step(i)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    distinct = []
+    for i in range(len(xs)):
+        step(i)
+        distinct.append(len(np.unique(sel.cpu().numpy())))
+    nd = float(np.mean(distinct))
+    lb = layer_bytes(cfg, nd)
+    row = {"T": T, "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_step": round(ms, 4),
+           "distinct_experts": nd, "algorithmic_bytes": int(lb),
+           "hbm_frac": round(lb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    if T > 8:
+        fl = sum(prefill_flops(cfg, T).values())
+        row["mfma_flops"] = int(fl)
+        row["mfma_frac"] = round(fl / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)
+    layer.close()
+    return row
+
+
+def host_weights(w):
+    import numpy as np
+    f = lambda t: None if t is None else t.cpu().numpy().reshape(-1).copy()
+    return {"router": w.router_f16.cpu().numpy().view(np.uint16).reshape(-1).copy(), "bias": f(w.bias),
+            "gate": f(w.gate), "up": f(w.up), "down": f(w.down), "sh_gate": f(w.sh_gate), "sh_up": f(w.sh_up),
+            "sh_down": f(w.sh_down)}
+
+
+def cpu_baseline(case, hw, xs, seconds, cores):
     """The CPU oracle (a restatement of the reference arithmetic) on a
     bounded sample of the same workload."""
-    import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_ref as O
-    f = lambda t: None if t is None else t.cpu().numpy().reshape(-1).copy()
-    hw = {"router": w.router_f16.cpu().numpy().view(np.uint16).reshape(-1).copy(), "bias": f(w.bias),
-          "gate": f(w.gate), "up": f(w.up), "down": f(w.down), "sh_gate": f(w.sh_gate), "sh_up": f(w.sh_up),
-          "sh_down": f(w.sh_down)}
     T = xs[0].shape[0]
-    O.moe_forward(case.cfg, hw, xs[0].cpu().numpy(), T, cores)  # warm
+    xh = [x.cpu().numpy() for x in xs]
+    O.moe_forward(case.cfg, hw, xh[0], T, cores)  # warm
     n = 0
     t0 = time.perf_counter()
     while True:
-        O.moe_forward(case.cfg, hw, xs[n % len(xs)].cpu().numpy(), T, cores)
+        O.moe_forward(case.cfg, hw, xh[n % len(xh)], T, cores)
         n += 1
         el = time.perf_counter() - t0
         if el >= seconds or n >= 2000:
             break
     return {"value": n * T / el, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"{n} layer calls x {T} token(s) of config {case.name} in {el:.1f} s "
-                      f"(oracle/dsmoe_oracle.c, {cores} threads, layer-0 weights)"}
+                      f"(oracle/dsmoe_oracle.c, {cores} thread{'s' if cores > 1 else ''}, layer-0 weights)"}
 
 
 def main():
@@ -200,6 +291,9 @@ def main():
     ap.add_argument("--prefill-config", default="c5",
                     help="config of the prefill measurement added to the line ('none' to skip)")
     ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--other-configs", default="c1,c3,c4",
+                    help="configs also timed on the same path, reported under other_configs ('none' to skip)")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the on-box MFMA / HBM peak probes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: every box in this build has one MI355X and the MoE path is "
@@ -283,11 +377,31 @@ def main():
         print(f"[bench] prefill {args.prefill_config}", file=sys.stderr, flush=True)
         prefill = prefill_bench(C.CASES[args.prefill_config], args.prefill_steps, 2, dev)
 
+    others = {}
+    if args.other_configs != "none":
+        for name in [n for n in args.other_configs.split(",") if n and n != args.config]:
+            oc = C.CASES[name]
+            print(f"[bench] config {name}", file=sys.stderr, flush=True)
+            same = oc.cfg == cfg and oc.seed == case.seed and oc.d_ff_real == case.d_ff_real
+            ow = layers[0] if same else C.make_weights(oc, layer=0, device=dev)
+            others[name] = config_bench(oc, ow, 50 if oc.T <= 8 else 20, 5, dev)
+            if not same:
+                del ow
+
+    peaks = None
+    if not args.no_peaks:
+        print("[bench] peak probes", file=sys.stderr, flush=True)
+        peaks = box_peaks(dev)
+
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        cores = min(16, os.cpu_count() or 1)
-        cpu = cpu_baseline(case, layers[0], xs, args.cpu_seconds, cores)
+        hw = host_weights(layers[0])
+        cpu = cpu_baseline(case, hw, xs, args.cpu_seconds, 1)
+        multi = min(16, os.cpu_count() or 1)
+        cpu_multi = cpu_baseline(case, hw, xs, args.cpu_seconds / 2, multi)
+        cpu["host"] = host_info()
+        cpu[f"value_{multi}_threads"] = round(cpu_multi["value"], 2)
 
     out = {
         "metric": "MoE-layer tokens/s & % of HBM/MFMA roofline, decode B=1 and prefill 2048",
@@ -314,6 +428,8 @@ def main():
                            "frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
         "stages": stage_rows,
         "prefill": prefill,
+        "other_configs": others,
+        "box_peaks": peaks,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
