@@ -294,6 +294,7 @@ def main():
     ap.add_argument("--other-configs", default="c1,c3,c4",
                     help="configs also timed on the same path, reported under other_configs ('none' to skip)")
     ap.add_argument("--no-peaks", action="store_true", help="skip the on-box MFMA / HBM peak probes")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timing of the decode step")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: every box in this build has one MI355X and the MoE path is "
@@ -337,6 +338,33 @@ def main():
     stop.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / args.steps
+
+    # the same steps replayed from HIP graphs (one captured call per weight set
+    # and activation slot; dsmoe_forward allocates nothing and sets no memory)
+    graph_ms = None
+    if T <= 8 and not args.no_graph:
+        graphs = []
+        cs = torch.cuda.Stream()
+        cs.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cs):
+            step(0)
+        torch.cuda.current_stream().wait_stream(cs)
+        nslots = L * 4
+        for i in range(nslots):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                step(i)
+            graphs.append(gr)
+        for i in range(args.warmup):
+            graphs[i % nslots].replay()
+        torch.cuda.synchronize()
+        start.record()
+        for i in range(args.steps):
+            graphs[i % nslots].replay()
+        stop.record()
+        torch.cuda.synchronize()
+        graph_ms = start.elapsed_time(stop) / args.steps
+        del graphs
 
     # per-stage timing pass (events around each stage on the launch stream)
     nprof = min(args.steps, 100)
@@ -427,6 +455,9 @@ def main():
         "layer_roofline": {"algorithmic_bytes": int(lb), "achieved": round(layer_gbs, 1), "unit": "GB/s",
                            "frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
         "stages": stage_rows,
+        "graph_replay": None if graph_ms is None else {
+            "ms_per_step": round(graph_ms, 5), "tokens_per_s": round(T / (graph_ms * 1e-3), 1),
+            "note": "the same steps captured as HIP graphs (one per weight set and activation slot) and replayed"},
         "prefill": prefill,
         "other_configs": others,
         "box_peaks": peaks,

@@ -631,3 +631,41 @@ def test_hc_expand_bitexact(gpu, n, n_hc, T, has_add, mix, offset):
     torch.cuda.synchronize()
     want = O.hc_expand(bo, ba if has_add else None, res, split, n, n_hc, T, mix, has_add)
     assert bits_equal(np_(out).reshape(T, n_hc, n), want)
+
+
+@pytest.mark.parametrize("name", ["c2", "c1"])
+def test_decode_layer_in_a_hip_graph(gpu, name):
+    """The three decode launches captured in one HIP graph (no memset or
+    allocation inside dsmoe_forward) and replayed with eager layer calls and
+    synchronizations between the replays: every replay equals the eager call
+    on the same input, bit for bit."""
+    import torch
+    case = C.CASES[name]
+    cfg = case.cfg
+    d, k = cfg.d_model, cfg.top_k
+    say(f"hip graph decode {name}")
+    w = C.make_weights(case, device=gpu)
+    xs = [C.make_x(case, T=1, step=s, device=gpu) for s in range(4)]
+    lay, ref = dsmoe.MoeLayer(cfg, 1), dsmoe.MoeLayer(cfg, 1)
+    x = xs[0].clone()
+    so, ro = torch.empty(1, d, device=gpu), torch.empty(1, d, device=gpu)
+    sel, wt = torch.empty(1, k, dtype=torch.int32, device=gpu), torch.empty(1, k, device=gpu)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        lay.forward(w, x, so, ro, sel, wt)  # warm (code objects loaded before the capture)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        lay.forward(w, x, so, ro, sel, wt)
+    for rep in range(6):
+        x.copy_(xs[rep % 4])
+        g.replay()
+        so2, ro2 = torch.empty(1, d, device=gpu), torch.empty(1, d, device=gpu)
+        sel2, wt2 = torch.empty(1, k, dtype=torch.int32, device=gpu), torch.empty(1, k, device=gpu)
+        ref.forward(w, xs[rep % 4], so2, ro2, sel2, wt2)
+        torch.cuda.synchronize()
+        for a_, b_ in ((so, so2), (ro, ro2), (sel, sel2), (wt, wt2)):
+            assert bits_equal(np_(a_), np_(b_)), f"replay {rep} differs from the eager call"
+    lay.close()
+    ref.close()
