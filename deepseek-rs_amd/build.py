@@ -41,7 +41,7 @@ def build_host():
          "-o", obj])
     run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-ffp-contract=off", "-Wall",
          "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"),
-         "-I", CSRC, os.path.join(CSRC, "dsmoe_host.cpp"), obj, "-o", out,
+         "-I", CSRC, os.path.join(CSRC, "dsmoe_host.cpp"), os.path.join(CSRC, "dsmoe_gguf.cpp"), obj, "-o", out,
          "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath," + os.path.join(ROCM, "lib"),
          "-ldl", "-lpthread"])
     return out

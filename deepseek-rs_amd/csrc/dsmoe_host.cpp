@@ -289,6 +289,11 @@ int validate_cfg(const dsmoe_config* c) {
 
 }  // namespace
 
+namespace dsm_gguf {
+// The GGUF reader (dsmoe_gguf.cpp) reports through the same last-error slot.
+int fail(int code, const std::string& msg) { return ::fail(code, msg); }
+}  // namespace dsm_gguf
+
 // ==========================================================================
 // C ABI
 // ==========================================================================

@@ -31,6 +31,8 @@ EXPORTED = [
     "dsmoe_synth_tensor_host", "dsmoe_stage_name", "dsmoe_set_profiling", "dsmoe_profile_read",
     "dsmoe_q8k_quantize_h", "dsmoe_gate_up_mid_sorted", "dsmoe_down_sorted", "dsmoe_q8_0_quantize_h",
     "dsmoe_q8_0_gemm",
+    "dsmoe_gguf_open", "dsmoe_gguf_close", "dsmoe_gguf_tensor_count", "dsmoe_gguf_data_offset", "dsmoe_gguf_tensor_at",
+    "dsmoe_gguf_find", "dsmoe_gguf_kv_u32", "dsmoe_gguf_kv_i32_array", "dsmoe_gguf_moe_layer",
 ]
 GROUPED_TILE_M = 64  # DSMOE_GROUPED_TILE_M
 STAGE_COUNT = 9

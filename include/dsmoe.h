@@ -44,7 +44,8 @@ enum {
   DSMOE_ERR_UNSUPPORTED = 2, /* valid but outside what the kernels handle */
   DSMOE_ERR_HIP = 3,         /* HIP runtime error */
   DSMOE_ERR_NOMEM = 4,       /* device allocation failed */
-  DSMOE_ERR_MODULE = 5       /* kernel code object missing / unloadable */
+  DSMOE_ERR_MODULE = 5,      /* kernel code object missing / unloadable */
+  DSMOE_ERR_NOT_FOUND = 6    /* GGUF tensor or key absent */
 };
 
 /* Layer configuration.  The reference hard-codes d=4096, I=2048, E=256,
@@ -301,6 +302,48 @@ int dsmoe_synth_tensor(void* out, int32_t fmt, uint64_t seed, uint64_t tensor_id
 int dsmoe_synth_tensor_host(void* out_host, int32_t fmt, uint64_t seed, uint64_t tensor_id, int64_t n_mats,
                             int32_t rows, int32_t cols, int32_t rows_real, int32_t cols_real, float sigma,
                             int32_t nthreads);
+
+/* --------------------------------------------------------------------- */
+/* GGUF expert tensors (engine/src/gguf.rs, engine/src/model.rs:28-104)    */
+/* --------------------------------------------------------------------- */
+/* A read-only GGUF v2/v3 file, memory-mapped: the metadata section is
+ * walked (values skipped by type; an unknown metadata type, tensor type, bad
+ * magic, a version outside 2..3, or a tensor past the end of the file is
+ * DSMOE_ERR_INVALID), tensor infos are read, and the data section starts at
+ * the next 32-byte boundary after them.  Tensor data are host pointers into
+ * the mapping, valid until dsmoe_gguf_close; the caller copies what it needs
+ * to the device. */
+typedef struct dsmoe_gguf dsmoe_gguf;
+enum { DSMOE_GGUF_F32 = 0, DSMOE_GGUF_F16 = 1, DSMOE_GGUF_Q8_0 = 8, DSMOE_GGUF_Q2_K = 10, DSMOE_GGUF_Q4_K = 12,
+       DSMOE_GGUF_IQ2_XXS = 16, DSMOE_GGUF_I32 = 26 };
+typedef struct dsmoe_gguf_tensor {
+  const char* name;  /* owned by the file handle */
+  int32_t type;      /* DSMOE_GGUF_* */
+  int32_t n_dims;    /* 1..4; unused dims read 1 */
+  uint64_t dims[4];  /* as stored in the file */
+  uint64_t offset;   /* from the start of the data section */
+  uint64_t bytes;    /* TensorType::byte_size of the element count (model.rs:80-85) */
+  const void* data;  /* host pointer into the mapping */
+} dsmoe_gguf_tensor;
+int dsmoe_gguf_open(const char* path, dsmoe_gguf** out);
+int dsmoe_gguf_close(dsmoe_gguf* g);
+int64_t dsmoe_gguf_tensor_count(const dsmoe_gguf* g);
+uint64_t dsmoe_gguf_data_offset(const dsmoe_gguf* g);
+int dsmoe_gguf_tensor_at(const dsmoe_gguf* g, int64_t index, dsmoe_gguf_tensor* out);
+/* GgufFile::find; DSMOE_ERR_NOT_FOUND when no tensor has the name. */
+int dsmoe_gguf_find(const dsmoe_gguf* g, const char* name, dsmoe_gguf_tensor* out);
+/* GgufFile::read_kv_u32 / read_kv_i32_array (a key of another type is not
+ * found; *count is the array length, at most cap values are copied). */
+int dsmoe_gguf_kv_u32(const dsmoe_gguf* g, const char* key, uint32_t* out);
+int dsmoe_gguf_kv_i32_array(const dsmoe_gguf* g, const char* key, int32_t* out, int64_t cap, int64_t* count);
+/* The MoE tensors of one layer, by the engine's names (engine.rs:175-187):
+ * out[0..9] = blk.N.{ffn_gate_inp.weight, exp_probs_b.bias,
+ * ffn_gate_exps.weight, ffn_up_exps.weight, ffn_down_exps.weight,
+ * ffn_gate_shexp.weight, ffn_up_shexp.weight, ffn_down_shexp.weight,
+ * ffn_gate_tid2eid.weight, ffn_norm.weight}; bit i of *present says out[i]
+ * was found (absent entries are zeroed). */
+#define DSMOE_GGUF_MOE_TENSORS 10
+int dsmoe_gguf_moe_layer(const dsmoe_gguf* g, int32_t layer, dsmoe_gguf_tensor* out, int32_t* present);
 
 #ifdef __cplusplus
 }

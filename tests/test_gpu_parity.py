@@ -669,3 +669,28 @@ def test_decode_layer_in_a_hip_graph(gpu, name):
             assert bits_equal(np_(a_), np_(b_)), f"replay {rep} differs from the eager call"
     lay.close()
     ref.close()
+
+
+def test_layer_from_gguf_file(gpu, tmp_path):
+    """A layer written to a GGUF file, mapped by dsmoe_gguf_open and uploaded:
+    dsmoe_forward on it gives the bits of the same layer from memory."""
+    import torch
+    from dsmoe import gguf as G
+    case = C.CASES["c1"]
+    cfg = case.cfg
+    say("layer from gguf c1")
+    w = C.make_weights(case, device=gpu)
+    p = tmp_path / "c1.gguf"
+    G.write(p, G.moe_layer_tensors(cfg, w, layer=0))
+    with G.GgufFile(p) as g:
+        w2 = G.layer_weights(g, 0, device=gpu)
+    x = C.make_x(case, T=3, device=gpu)
+    outs = []
+    for ww in (w, w2):
+        lay = dsmoe.MoeLayer(cfg, 3)
+        so, ro = torch.empty(3, cfg.d_model, device=gpu), torch.empty(3, cfg.d_model, device=gpu)
+        lay.forward(ww, x, so, ro)
+        torch.cuda.synchronize()
+        outs.append((np_(so), np_(ro)))
+        lay.close()
+    assert bits_equal(outs[0][0], outs[1][0]) and bits_equal(outs[0][1], outs[1][1])
