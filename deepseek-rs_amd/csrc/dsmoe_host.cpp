@@ -84,7 +84,7 @@ const std::vector<uint8_t>& lvlmap_host() {
 enum Kern { K_PREP, K_ROUTER_SELECT, K_UP, K_MIDQ, K_DN, K_SWIGLU, K_MOE_SUM, K_DISPATCH, K_SYNTH,
             K_GU_GROUPED, K_DN_GROUPED, K_Q80_GEMM_SWIGLU, K_Q80_GEMM,
             K_ROUTER_TILE, K_UP_ROWS, K_DN_ROWS, K_Q80_GEMM_SWIGLU_J7, K_Q80_GEMM_J7, K_Q80_GEMM_SWIGLU_J2,
-            K_Q80_GEMM_J2, K_HC_EXPAND, K_PROBE_MFMA, K_PROBE_READ, K_UP_EM, K_DN_EM, K_Q80_COMBINE, K_COUNT };
+            K_Q80_GEMM_J2, K_HC_EXPAND, K_PROBE_MFMA, K_PROBE_READ, K_UP_EM, K_DN_EM, K_Q80_COMBINE, K_SELECT_HASH, K_COUNT };
 const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_up", "dsmoe_midq", "dsmoe_dn",
                                    "dsmoe_swiglu", "dsmoe_moe_sum", "dsmoe_dispatch", "dsmoe_synth",
                                    "dsmoe_gu_grouped", "dsmoe_dn_grouped", "dsmoe_q80_gemm_swiglu", "dsmoe_q80_gemm",
@@ -92,9 +92,9 @@ const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_u
                                    "dsmoe_up_rows", "dsmoe_dn_rows", "dsmoe_q80_gemm_swiglu_j7", "dsmoe_q80_gemm_j7",
                                    "dsmoe_q80_gemm_swiglu_j2", "dsmoe_q80_gemm_j2", "dsmoe_hc_expand",
                                    "dsmoe_probe_mfma", "dsmoe_probe_read", "dsmoe_up_em", "dsmoe_dn_em",
-                                   "dsmoe_q80_combine"};
+                                   "dsmoe_q80_combine", "dsmoe_router_select_hash"};
 // code object of each kernel: 0 = dsmoe_kernels.hsaco, 1 = dsmoe_gemm.hsaco (same directory)
-const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0, 1, 1, 0, 0, 1};
+const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0, 1, 1, 0, 0, 1, 0};
 static_assert(DSMOE_GROUPED_TILE_M == kGuBM, "header and kernels disagree on the grouped tile");
 
 extern "C" int dsmoe_noalloc_setup(void** ptr, size_t* bytes);  // dsmoe_noalloc.hip
@@ -368,6 +368,17 @@ int dsmoe_router_select(const dsmoe_config* cfg, const float* logits, const floa
                      cfg->top_k, cfg->n_group > 1 ? cfg->n_group : 1, cfg->topk_group, cfg->has_bias ? 1 : 0,
                      cfg->route_scale};
   return launch(K_ROUTER_SELECT, dim3(T), dim3(256), select_lds(cfg->n_expert), stream, a);
+}
+
+int dsmoe_router_select_hash(const dsmoe_config* cfg, const float* logits, const int32_t* hash, int32_t hash_rows,
+                             const int32_t* tokens, int32_t token_scalar, int32_t T, float* probs, int32_t* selected,
+                             float* weights, dsmoe_stream_t stream) {
+  if (!cfg || !logits || !hash || !selected || !weights) return fail(DSMOE_ERR_INVALID, "router_select_hash: null pointer");
+  if (T < 0 || hash_rows < 1 || cfg->n_expert < 1 || cfg->top_k < 1)
+    return fail(DSMOE_ERR_INVALID, "router_select_hash: bad shape");
+  HashSelectArgs a{logits, hash, tokens, probs, selected, weights, token_scalar, hash_rows, T, cfg->n_expert,
+                   cfg->top_k, cfg->route_scale};
+  return launch(K_SELECT_HASH, dim3(T), dim3(256), 0, stream, a);
 }
 
 static int midq_impl(const Q8KArgs* qa, const Q8KArgs* qb, const Q80Args* q80, dsmoe_stream_t stream) {
@@ -754,6 +765,10 @@ struct dsmoe_ctx {
   uint32_t* g_tile_experts = nullptr;
   uint32_t* g_tile_starts = nullptr;
   float* q80_part = nullptr;     // split shared-expert GEMM partials, [kQ80MaxSplit][min(T, 256)][cols]
+  // hash routing (dsmoe_set_hash_routing): table [hash_rows][k], token ids [T]
+  const int32_t* hash = nullptr;
+  const int32_t* hash_tokens = nullptr;
+  int32_t hash_rows = 0;
   // mid row counters of the fused mid quantization in dsmoe_up_rows:
   // [kMaxDecodeT*k*(I/256)] routed, then [kMaxDecodeT*ceil(I_s/256)] shared;
   // zero between launches (the workgroup completing a block resets its word)
@@ -814,6 +829,15 @@ const char* dsmoe_stage_name(int32_t stage) {
   static const char* names[DSMOE_STAGE_COUNT] = {"prep", "select", "up", "midq", "dn",
                                                  "gu_grouped", "shared_up", "dn_grouped", "shared_dn"};
   return (stage >= 0 && stage < DSMOE_STAGE_COUNT) ? names[stage] : "?";
+}
+
+int dsmoe_set_hash_routing(dsmoe_ctx* c, const int32_t* hash, int32_t hash_rows, const int32_t* tokens) {
+  if (!c) return fail(DSMOE_ERR_INVALID, "set_hash_routing: ctx is NULL");
+  if (hash && hash_rows < 1) return fail(DSMOE_ERR_INVALID, "set_hash_routing: hash_rows < 1");
+  c->hash = hash;
+  c->hash_rows = hash ? hash_rows : 0;
+  c->hash_tokens = hash ? tokens : nullptr;
+  return DSMOE_OK;
 }
 
 int dsmoe_set_profiling(dsmoe_ctx* c, int32_t enable) {
@@ -976,10 +1000,14 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // In the row-streaming path every routed gate/up workgroup runs the
   // one-wave selection itself (no launch of its own).
   const bool up_rows = !grouped && up_rows_fits(d) && (cf.shared_fmt != 0 || q80_rows_fits(d));
-  const int fuse_p = up_rows ? select_wave_p(cf) : 0;
+  const int fuse_p = up_rows && !c->hash ? select_wave_p(cf) : 0;
   if (!fuse_p) {
     StageScope sc(c, DSMOE_STAGE_SELECT, stream);
-    DSM_TRY(dsmoe_router_select(&cf, c->logits, w->bias, T, nullptr, sel, wts, stream));
+    if (c->hash)  // hash routing (moe.rs:92-109): the token ids pick the experts
+      DSM_TRY(dsmoe_router_select_hash(&cf, c->logits, c->hash, c->hash_rows, c->hash_tokens, 0, T, nullptr, sel,
+                                       wts, stream));
+    else
+      DSM_TRY(dsmoe_router_select(&cf, c->logits, w->bias, T, nullptr, sel, wts, stream));
     if (grouped)  // moe_count/prefix/scatter_sorted_pairs + tiles (moe.rs:299-362, 547-596)
       DSM_TRY(dsmoe_dispatch(sel, P, E, em ? em_pairs() : kGuBM, c->g_counts, c->g_offsets, c->g_sorted,
                              c->g_tile_offsets, c->g_tile_experts, c->g_tile_starts, stream));

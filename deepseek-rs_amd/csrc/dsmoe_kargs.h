@@ -24,6 +24,18 @@ struct RouterSelectArgs {
   float route_scale;
 };
 
+// Hash routing (moe.rs:92-109): experts from a token-id table.
+struct HashSelectArgs {
+  const float* logits;    // [T][E]
+  const int32_t* hash;    // [hash_rows][k]
+  const int32_t* tokens;  // [T] or null (token_scalar for every token)
+  float* probs;           // [T][E] or null
+  int32_t* selected;      // [T][k]
+  float* weights;         // [T][k]
+  int32_t token_scalar, hash_rows, T, E, k;
+  float route_scale;
+};
+
 struct Q8KArgs {
   const float* x;  // [rows][in_dim]
   uint8_t* out;    // [rows][in_dim/256] x 292 B

@@ -2026,6 +2026,29 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_dn_em(const DnEmArgs a) 
   role_down_em(a, blockIdx.x % a.tiles, blockIdx.x / a.tiles, smem);
 }
 
+// Hash routing (moe.rs:92-109, weights :143-159), one workgroup per token:
+// the probabilities of all experts, then thread 0 reads the token's row of
+// the table and normalises the weights in slot order.
+extern "C" __global__ __launch_bounds__(256) void dsmoe_router_select_hash(const HashSelectArgs a) {
+  const int t = blockIdx.x, tid = threadIdx.x;
+  if (a.probs)
+    for (int e = tid; e < a.E; e += 256)
+      a.probs[(size_t)t * a.E + e] = __builtin_sqrtf(softplus_dsm(a.logits[(size_t)t * a.E + e]));
+  if (tid != 0) return;
+  int tok = a.tokens ? a.tokens[t] : a.token_scalar;
+  if (tok < 0 || tok >= a.hash_rows) tok = 0;
+  float sum = 0.0f;
+  for (int j = 0; j < a.k; j++) {
+    const int e = a.hash[(size_t)tok * a.k + j];
+    const float v = (e >= 0 && e < a.E) ? __builtin_sqrtf(softplus_dsm(a.logits[(size_t)t * a.E + e])) : 0.0f;
+    a.selected[(size_t)t * a.k + j] = e;
+    a.weights[(size_t)t * a.k + j] = v;
+    sum += v;
+  }
+  if (sum < 6.103515625e-5f) sum = 6.103515625e-5f;
+  for (int j = 0; j < a.k; j++) a.weights[(size_t)t * a.k + j] = a.weights[(size_t)t * a.k + j] / (sum / a.route_scale);
+}
+
 extern "C" __global__ __launch_bounds__(256) void dsmoe_router_select(const RouterSelectArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   role_select<false>(a, blockIdx.x, smem);

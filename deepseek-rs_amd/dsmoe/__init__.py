@@ -33,6 +33,7 @@ EXPORTED = [
     "dsmoe_q8_0_gemm",
     "dsmoe_gguf_open", "dsmoe_gguf_close", "dsmoe_gguf_tensor_count", "dsmoe_gguf_data_offset", "dsmoe_gguf_tensor_at",
     "dsmoe_gguf_find", "dsmoe_gguf_kv_u32", "dsmoe_gguf_kv_i32_array", "dsmoe_gguf_moe_layer",
+    "dsmoe_router_select_hash", "dsmoe_set_hash_routing",
 ]
 GROUPED_TILE_M = 64  # DSMOE_GROUPED_TILE_M
 STAGE_COUNT = 9
@@ -78,6 +79,8 @@ def lib():
         "dsmoe_forward": ([vp, ctypes.POINTER(Weights), vp, i32, vp, vp, vp, vp, vp], i32),
         "dsmoe_gate_up_mid_em": ([vp] * 10 + [i32, i32, i32, i32, i32, i32, f32, vp], i32),
         "dsmoe_down_em": ([vp] * 8 + [i32, i32, i32, i32, i32, vp], i32),
+        "dsmoe_router_select_hash": ([ctypes.POINTER(Config), vp, vp, i32, vp, i32, i32, vp, vp, vp, vp], i32),
+        "dsmoe_set_hash_routing": ([vp, vp, i32, vp], i32),
         "dsmoe_probe": ([i32, vp, ctypes.c_size_t, ctypes.c_int64, vp, vp], i32),
         "dsmoe_hc_expand": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp], i32),
         "dsmoe_forward_noalloc": ([ctypes.POINTER(Config), ctypes.POINTER(Weights), vp, i32, vp, vp, vp, vp, vp], i32),
@@ -324,6 +327,14 @@ def down_em(w, mq, sorted_pairs, offsets, tile_offsets, tile_experts, tile_start
                               _p(tile_starts), _p(down_out), d, I, E, pairs, block_m, _stream(stream)))
 
 
+def router_select_hash(cfg, logits, hash_table, hash_rows, tokens, token_scalar, T, probs, selected, weights,
+                       stream=None):
+    """router_select with hash_mode = 1 (moe.rs:92-109): experts from the token-id table."""
+    c = cfg.c()
+    check(lib().dsmoe_router_select_hash(ctypes.byref(c), _p(logits), _p(hash_table), hash_rows, _p(tokens),
+                                         token_scalar, T, _p(probs), _p(selected), _p(weights), _stream(stream)))
+
+
 def probe(kind, src, nbytes, iters, sink, stream=None):
     """dsmoe_probe: kind 0 = dense f16 MFMA loop, 1 = HBM read of nbytes of src."""
     check(lib().dsmoe_probe(int(kind), _p(src), int(nbytes), int(iters), _p(sink), _stream(stream)))
@@ -361,6 +372,11 @@ class MoeLayer:
     @property
     def scratch_bytes(self):
         return int(lib().dsmoe_scratch_bytes(self._ctx))
+
+    def set_hash_routing(self, hash_table=None, hash_rows=0, tokens=None):
+        """Route later forwards by token id (hash_table [hash_rows][k], tokens [T]); None returns to top-k."""
+        self._hash_keep = (hash_table, tokens)  # the device buffers must outlive the forwards
+        check(lib().dsmoe_set_hash_routing(self._ctx, _p(hash_table), hash_rows, _p(tokens)))
 
     def set_profiling(self, on: bool):
         check(lib().dsmoe_set_profiling(self._ctx, int(on)))

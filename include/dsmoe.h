@@ -122,6 +122,15 @@ int dsmoe_forward_noalloc(const dsmoe_config* cfg, const dsmoe_weights* w, const
                           float* shared_out, float* routed_out, int32_t* selected, float* weights,
                           dsmoe_stream_t stream);
 
+/* Hash routing for the layers that route by token id (the reference's
+ * hash_mode, moe.rs:92-109, with the table blk.N.ffn_gate_tid2eid): when
+ * `hash` (device, i32 [hash_rows][top_k]) is set, every later dsmoe_forward
+ * on this context takes the experts of token t from row tokens[t] of the
+ * table (tokens: device i32 [T], read at each forward; NULL = row 0) instead
+ * of the top-k selection; the weights are computed as in
+ * dsmoe_router_select_hash.  hash = NULL returns to top-k routing. */
+int dsmoe_set_hash_routing(dsmoe_ctx* ctx, const int32_t* hash, int32_t hash_rows, const int32_t* tokens);
+
 /* Per-stage timing of dsmoe_forward (no reference counterpart: the
  * reference has no tracing).  When enabled, every stage of the forward is
  * bracketed by hipEvents on the caller's stream; dsmoe_profile_read waits
@@ -249,6 +258,17 @@ int dsmoe_moe_sum(const float* down, float* out, int32_t d, int32_t k, int32_t T
  * with 16-byte loads, 8 workgroups per CU.  `sink` (device, >= 8 floats per
  * CU) is written only on a data-dependent branch. */
 int dsmoe_probe(int32_t kind, const void* src, size_t bytes, int64_t iters, float* sink, dsmoe_stream_t stream);
+
+/* router_select with hash_mode = 1 (engine/src/kernels/moe.rs:92-109,
+ * weights :143-159): selected[t][j] = hash[tok][j] with tok = tokens[t]
+ * (token_scalar when tokens is NULL; an id outside [0, hash_rows) uses row
+ * 0); probs as in dsmoe_router_select; weight j = probs[t][selected] (0 for
+ * an id outside [0, n_expert)) / (max(sum in slot order, 2^-14) /
+ * route_scale).  The reference hard-codes k = 6, E = 256, scale 1.5; here
+ * they come from cfg.  The correction bias plays no part. */
+int dsmoe_router_select_hash(const dsmoe_config* cfg, const float* logits, const int32_t* hash, int32_t hash_rows,
+                             const int32_t* tokens, int32_t token_scalar, int32_t T, float* probs,
+                             int32_t* selected, float* weights, dsmoe_stream_t stream);
 
 /* hc_expand (engine/src/kernels/hc.rs:212-259), the FFN residual merge that
  * consumes the layer's outputs (session.rs:2157-2175: block_out =

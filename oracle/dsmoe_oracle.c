@@ -26,6 +26,8 @@
  *                                  weights sum to route_scale; ratio preservation
  *   grouped routing (n_group > 1)  brute force over all group subsets (no reference
  *                                  counterpart: the reference has no group-limited top-k)
+ *   or_router_select_hash          plain-Python restatement of the table lookup on
+ *                                  out-of-range tokens and ids (moe.rs:92-109)
  *   or_dispatch                    numpy stable argsort; prefix sums
  *   or_moe_sum                     f32 values whose sum depends on the slot order
  *   or_hc_expand                   dyadic inputs (exact in f32) vs the float64 formula, with
@@ -349,6 +351,33 @@ static void insert_topk(int32_t* sel, int n, const float* score, int e) {
 /* moe.rs:177-287 router_select_parallel (n_group == 1), generalised to
  * E experts / top-k / route_scale; n_group > 1 adds group-limited
  * selection (group score = best + second best biased score). */
+/* Hash routing (moe.rs:92-109 with the weights of :143-159): the token id
+ * picks the k experts from the table (token ids outside [0, hash_rows) use
+ * row 0; no token array = token_scalar for every token); probs are
+ * sqrt(softplus(logit)) as in top-k routing; weight j = probs[e_j] (0 for an
+ * id outside [0, E)) / (max(sum in slot order, 2^-14) / route_scale). */
+void or_router_select_hash(const or_config* c, const float* logits, const int32_t* hash, int hash_rows,
+                           const int32_t* tokens, int token_scalar, int T, float* probs, int32_t* selected,
+                           float* weights) {
+  const int E = c->n_expert, K = c->top_k;
+  for (int t = 0; t < T; t++) {
+    if (probs)
+      for (int e = 0; e < E; e++) probs[(size_t)t * E + e] = sqrtf(or_softplus(logits[(size_t)t * E + e]));
+    int tok = tokens ? tokens[t] : token_scalar;
+    if (tok < 0 || tok >= hash_rows) tok = 0;
+    float sum = 0.0f;
+    for (int j = 0; j < K; j++) {
+      const int e = hash[(size_t)tok * K + j];
+      selected[(size_t)t * K + j] = e;
+      const float v = (e >= 0 && e < E) ? sqrtf(or_softplus(logits[(size_t)t * E + e])) : 0.0f;
+      weights[(size_t)t * K + j] = v;
+      sum += v;
+    }
+    if (sum < 6.103515625e-5f) sum = 6.103515625e-5f;
+    for (int j = 0; j < K; j++) weights[(size_t)t * K + j] /= sum / c->route_scale;
+  }
+}
+
 void or_router_select(const or_config* c, const float* logits, const float* bias, int T,
                       float* probs, int32_t* selected, float* weights) {
   int E = c->n_expert, K = c->top_k;

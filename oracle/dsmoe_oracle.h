@@ -54,6 +54,9 @@ void or_q8_0_quantize(const float* x, int8_t* xq, float* xscale, int in_dim, int
 
 /* dense pieces */
 void or_router_logits(const uint16_t* w, const float* x, float* out, int d, int E, int T, int nthreads);
+void or_router_select_hash(const or_config* c, const float* logits, const int32_t* hash, int hash_rows,
+                           const int32_t* tokens, int token_scalar, int T, float* probs, int32_t* selected,
+                           float* weights);
 void or_router_select(const or_config* c, const float* logits, const float* bias, int T,
                       float* probs, int32_t* selected, float* weights);
 void or_q8_0_matvec(const uint8_t* w, const int8_t* xq, const float* xscale, float* out,

@@ -61,6 +61,7 @@ def load():
         "or_gate_up_mid": ([vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, i32], None),
         "or_down": ([vp, vp, vp, vp, i32, i32, i32, i32, i32], None),
         "or_moe_sum": ([vp, vp, i32, i32, i32], None),
+        "or_router_select_hash": ([vp, vp, vp, i32, vp, i32, i32, vp, vp, vp], None),
         "or_hc_expand": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, i32], None),
         "or_dispatch": ([vp, i32, i32, i32, vp, vp, vp, vp, vp, vp], None),
         "or_moe_forward": ([ctypes.POINTER(OrConfig), vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, vp, vp, vp, i32], i32),
@@ -102,6 +103,19 @@ def router_select(mcfg, logits, bias, T):
     c = cfg_of(mcfg)
     load().or_router_select(ctypes.byref(c), P(np.ascontiguousarray(logits, np.float32)),
                             P(None if bias is None else np.ascontiguousarray(bias, np.float32)), T, P(probs), P(sel), P(w))
+    return probs.reshape(T, E), sel.reshape(T, K), w.reshape(T, K)
+
+
+def router_select_hash(mcfg, logits, hash_table, hash_rows, tokens, token_scalar, T):
+    E, K = mcfg.n_expert, mcfg.top_k
+    probs = np.zeros(T * E, np.float32)
+    sel = np.zeros(T * K, np.int32)
+    w = np.zeros(T * K, np.float32)
+    c = cfg_of(mcfg)
+    load().or_router_select_hash(ctypes.byref(c), P(np.ascontiguousarray(logits, np.float32)),
+                                 P(np.ascontiguousarray(hash_table, np.int32)), hash_rows,
+                                 P(None if tokens is None else np.ascontiguousarray(tokens, np.int32)), token_scalar,
+                                 T, P(probs), P(sel), P(w))
     return probs.reshape(T, E), sel.reshape(T, K), w.reshape(T, K)
 
 

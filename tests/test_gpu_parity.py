@@ -694,3 +694,73 @@ def test_layer_from_gguf_file(gpu, tmp_path):
         outs.append((np_(so), np_(ro)))
         lay.close()
     assert bits_equal(outs[0][0], outs[1][0]) and bits_equal(outs[0][1], outs[1][1])
+
+
+def test_router_select_hash_bitexact(gpu):
+    """Hash routing on the GPU against the oracle, bit for bit: tokens
+    outside the table, negative tokens, table ids outside [0, E), the scalar
+    token when no token array is given."""
+    import torch
+    say("router_select_hash")
+    rng = np.random.default_rng(12)
+    E, k, rows, T = 256, 6, 129, 40
+    cfg = dsmoe.MoeConfig(d_model=512, d_ff=256, n_expert=E, top_k=k, route_scale=1.5, shared_fmt=-1)
+    logits = rng.normal(0, 2, (T, E)).astype(np.float32)
+    table = rng.integers(0, E, (rows, k)).astype(np.int32)
+    table[5, 0], table[6, 5] = -1, E
+    tokens = rng.integers(-3, rows + 3, T).astype(np.int32)
+    tokens[:3] = [5, 6, 2**31 - 1]
+    dl = torch.from_numpy(logits).to(gpu)
+    dt = torch.from_numpy(table).to(gpu)
+    for tok_arr in (tokens, None):
+        probs = torch.empty(T, E, device=gpu)
+        sel = torch.empty(T, k, dtype=torch.int32, device=gpu)
+        w = torch.empty(T, k, device=gpu)
+        dtok = None if tok_arr is None else torch.from_numpy(tok_arr).to(gpu)
+        dsmoe.router_select_hash(cfg, dl, dt, rows, dtok, 17, T, probs, sel, w)
+        p0, s0, w0 = O.router_select_hash(cfg, logits, table, rows, tok_arr, 17, T)
+        torch.cuda.synchronize()
+        assert np.array_equal(np_(sel), s0)
+        assert bits_equal(np_(w), w0) and bits_equal(np_(probs), p0)
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_layer_with_hash_routing(gpu, T):
+    """dsmoe_forward with hash routing set: the selection equals
+    dsmoe_router_select_hash on the layer's logits, and the routed output
+    equals the per-kernel entry points on that selection."""
+    import torch
+    case = C.CASES["c1"]
+    cfg = case.cfg
+    d, I, E, k = cfg.d_model, cfg.d_ff, cfg.n_expert, cfg.top_k
+    say(f"layer with hash routing T={T}")
+    w = C.make_weights(case, device=gpu)
+    x = C.make_x(case, T=T, device=gpu)
+    rng = np.random.default_rng(13 + T)
+    rows = 50
+    table = torch.from_numpy(rng.integers(0, E, (rows, k)).astype(np.int32)).to(gpu)
+    tokens = torch.from_numpy(rng.integers(0, rows, T).astype(np.int32)).to(gpu)
+    lay = dsmoe.MoeLayer(cfg, T)
+    lay.set_hash_routing(table, rows, tokens)
+    so, ro = torch.empty(T, d, device=gpu), torch.empty(T, d, device=gpu)
+    sel, wt = torch.empty(T, k, dtype=torch.int32, device=gpu), torch.empty(T, k, device=gpu)
+    lay.forward(w, x, so, ro, sel, wt)
+    logits = torch.empty(T, E, device=gpu)
+    dsmoe.router_logits(w.router_f16, x, logits, d, E, T)
+    s2, w2 = torch.empty(T, k, dtype=torch.int32, device=gpu), torch.empty(T, k, device=gpu)
+    dsmoe.router_select_hash(cfg, logits, table, rows, tokens, 0, T, None, s2, w2)
+    xq = torch.empty(T * (d // 256) * 292, dtype=torch.uint8, device=gpu)
+    dsmoe.q8k_quantize(x, xq, d, T)
+    m = torch.empty(T * k, I, device=gpu)
+    dsmoe.gate_up_mid(w.gate, w.up, xq, s2, w2, None, None, m, d, I, T, k, E, cfg.swiglu_clamp)
+    mq = torch.empty(T * k * (I // 256) * 292, dtype=torch.uint8, device=gpu)
+    dsmoe.q8k_quantize(m, mq, I, T * k)
+    ro2 = torch.empty(T, d, device=gpu)
+    dsmoe.down(w.down, mq, s2, None, ro2, d, I, T, k, E)
+    torch.cuda.synchronize()
+    assert np.array_equal(np_(sel), np_(s2)) and bits_equal(np_(wt), np_(w2))
+    assert bits_equal(np_(ro), np_(ro2))
+    lay.set_hash_routing(None)
+    lay.forward(w, x, so, ro, sel, wt)  # back to top-k
+    torch.cuda.synchronize()
+    lay.close()

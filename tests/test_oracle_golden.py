@@ -552,3 +552,37 @@ def test_hc_expand_float64_and_order(oracle):
                 float(split[t, 2 * n_hc + dst + s * n_hc]) * res[t, s].astype(np.float64) for s in range(n_hc))
             assert np.max(np.abs(got[t, dst] - w64)) < 1e-5 * (1 + np.max(np.abs(w64)))
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------- hash routing
+def test_router_select_hash_restated(oracle):
+    """or_router_select_hash against a plain restatement of moe.rs:92-109
+    and the weight normalisation :143-159: tokens outside the table and
+    negative tokens use row 0, ids outside [0, E) weigh 0, a token array of
+    None uses the scalar token, and the weights sum to route_scale."""
+    rng = np.random.default_rng(11)
+    E, k, rows, T = 32, 4, 10, 9
+    logits = rng.normal(0, 2, (T, E)).astype(np.float32)
+    table = rng.integers(0, E, (rows, k)).astype(np.int32)
+    table[3, 1] = -1
+    table[4, 2] = E + 3
+    tokens = np.array([0, 3, 4, 9, 10, -5, 2**31 - 1, 7, 4], np.int32)
+    cfg = _Cfg(E, k, scale=2.5)
+    probs, sel, w = oracle_ref.router_select_hash(cfg, logits, table, rows, tokens, 0, T)
+    p_ref, _, _ = oracle_ref.router_select(cfg, logits, None, T)
+    assert np.array_equal(probs.view(np.uint32), p_ref.view(np.uint32))
+    for t in range(T):
+        tok = tokens[t] if 0 <= tokens[t] < rows else 0
+        assert list(sel[t]) == list(table[tok])
+        v = [np.float32(probs[t, e]) if 0 <= e < E else np.float32(0) for e in table[tok]]
+        s = np.float32(0)
+        for x in v:
+            s = np.float32(s + x)
+        s = max(s, np.float32(6.103515625e-5))
+        want = np.array([np.float32(x / np.float32(s / np.float32(2.5))) for x in v], np.float32)
+        assert np.array_equal(w[t].view(np.uint32), want.view(np.uint32)), t
+    assert w[1, 1] == 0 and w[2, 2] == 0
+    ok = [t for t in range(T) if (sel[t] >= 0).all() and (sel[t] < E).all()]
+    assert np.allclose(w[ok].sum(1), 2.5, rtol=1e-5)
+    _, sel2, _ = oracle_ref.router_select_hash(cfg, logits, table, rows, None, 7, T)
+    assert (sel2 == table[7]).all()
