@@ -84,7 +84,7 @@ const std::vector<uint8_t>& lvlmap_host() {
 enum Kern { K_PREP, K_ROUTER_SELECT, K_UP, K_MIDQ, K_DN, K_SWIGLU, K_MOE_SUM, K_DISPATCH, K_SYNTH,
             K_GU_GROUPED, K_DN_GROUPED, K_Q80_GEMM_SWIGLU, K_Q80_GEMM,
             K_ROUTER_TILE, K_UP_ROWS, K_DN_ROWS, K_Q80_GEMM_SWIGLU_J7, K_Q80_GEMM_J7, K_Q80_GEMM_SWIGLU_J2,
-            K_Q80_GEMM_J2, K_HC_EXPAND, K_PROBE_MFMA, K_PROBE_READ, K_UP_EM, K_DN_EM, K_Q80_COMBINE, K_SELECT_HASH, K_COUNT };
+            K_Q80_GEMM_J2, K_HC_EXPAND, K_PROBE_MFMA, K_PROBE_READ, K_UP_EM, K_DN_EM, K_Q80_COMBINE, K_SELECT_HASH, K_RMS_NORM, K_HC_SPLIT_NORM, K_COUNT };
 const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_up", "dsmoe_midq", "dsmoe_dn",
                                    "dsmoe_swiglu", "dsmoe_moe_sum", "dsmoe_dispatch", "dsmoe_synth",
                                    "dsmoe_gu_grouped", "dsmoe_dn_grouped", "dsmoe_q80_gemm_swiglu", "dsmoe_q80_gemm",
@@ -92,9 +92,10 @@ const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_u
                                    "dsmoe_up_rows", "dsmoe_dn_rows", "dsmoe_q80_gemm_swiglu_j7", "dsmoe_q80_gemm_j7",
                                    "dsmoe_q80_gemm_swiglu_j2", "dsmoe_q80_gemm_j2", "dsmoe_hc_expand",
                                    "dsmoe_probe_mfma", "dsmoe_probe_read", "dsmoe_up_em", "dsmoe_dn_em",
-                                   "dsmoe_q80_combine", "dsmoe_router_select_hash"};
+                                   "dsmoe_q80_combine", "dsmoe_router_select_hash",
+                                   "dsmoe_rms_norm_plain", "dsmoe_hc_split_norm"};
 // code object of each kernel: 0 = dsmoe_kernels.hsaco, 1 = dsmoe_gemm.hsaco (same directory)
-const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0, 1, 1, 0, 0, 1, 0};
+const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0, 1, 1, 0, 0, 1, 0, 0, 0};
 static_assert(DSMOE_GROUPED_TILE_M == kGuBM, "header and kernels disagree on the grouped tile");
 
 extern "C" int dsmoe_noalloc_setup(void** ptr, size_t* bytes);  // dsmoe_noalloc.hip
@@ -348,7 +349,7 @@ int dsmoe_router_logits(const uint16_t* w, const float* x, float* out, int32_t d
                         dsmoe_stream_t stream) {
   if (!w || !x || !out) return fail(DSMOE_ERR_INVALID, "router_logits: null pointer");
   if (d <= 0 || d % 256 || E <= 0 || T < 0) return fail(DSMOE_ERR_INVALID, "router_logits: d must be a multiple of 256");
-  if (d > 8192) return fail(DSMOE_ERR_UNSUPPORTED, "router_logits: d must be <= 8192");
+  if (d > 65536) return fail(DSMOE_ERR_UNSUPPORTED, "router_logits: d must be <= 65536");
   RouterLogitsArgs a{w, x, out, d, E, T};
   return prep_impl(&a, nullptr, nullptr, stream);
 }
@@ -550,6 +551,25 @@ int dsmoe_probe(int32_t kind, const void* src, size_t bytes, int64_t iters, floa
     return launch(K_PROBE_READ, dim3(8u * cus), dim3(256), 0, stream, a);
   }
   return fail(DSMOE_ERR_INVALID, "probe: unknown kind");
+}
+
+int dsmoe_rms_norm_plain(const float* x, float* out, int32_t n, int32_t rows, float eps, dsmoe_stream_t stream) {
+  if (!x || !out) return fail(DSMOE_ERR_INVALID, "rms_norm_plain: null pointer");
+  if (n < 1 || rows < 0) return fail(DSMOE_ERR_INVALID, "rms_norm_plain: bad shape");
+  RmsNormArgs a{x, out, n, rows, eps};
+  return launch(K_RMS_NORM, dim3(rows), dim3(256), 0, stream, a);
+}
+
+int dsmoe_hc_split_norm(const float* mix, const float* scale, const float* base, const float* residual_hc,
+                        const float* norm_w, float* split, float* out, float* norm_out, int32_t n_embd, int32_t n_hc,
+                        int32_t n_rows, int32_t sinkhorn_iters, float eps, float norm_eps, dsmoe_stream_t stream) {
+  if (!mix || !scale || !base || !residual_hc || !norm_w || !split || !out || !norm_out)
+    return fail(DSMOE_ERR_INVALID, "hc_split_norm: null pointer");
+  if (n_hc != 4) return fail(DSMOE_ERR_UNSUPPORTED, "hc_split_norm: n_hc must be 4 (hc.rs:337)");
+  if (n_embd < 1 || n_rows < 0 || sinkhorn_iters < 0) return fail(DSMOE_ERR_INVALID, "hc_split_norm: bad shape");
+  HcSplitNormArgs a{mix, scale, base, residual_hc, norm_w, split, out, norm_out, n_embd, n_rows, sinkhorn_iters,
+                    eps, norm_eps};
+  return launch(K_HC_SPLIT_NORM, dim3(n_rows), dim3(256), 0, stream, a);
 }
 
 int dsmoe_hc_expand(const float* block_out, const float* block_add, const float* residual_hc, const float* split,

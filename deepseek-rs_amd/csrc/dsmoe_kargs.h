@@ -269,6 +269,28 @@ inline __host__ __device__ bool moe_sum_vec_ok(const MoeSumArgs& a) {
   return a.d % 4 == 0 && (((uintptr_t)a.down | (uintptr_t)a.out) & 15) == 0;
 }
 
+// rms_norm_plain (norm.rs:14-63): one 256-thread workgroup per row.
+struct RmsNormArgs {
+  const float* x;
+  float* out;
+  int32_t n, rows;
+  float eps;
+};
+// hc_split_weighted_sum_norm_fused (hc.rs:313-398), n_hc = 4: one 256-thread
+// workgroup per row.
+struct HcSplitNormArgs {
+  const float* mix;          // [rows][24]
+  const float* scale;        // [3]
+  const float* base;         // [24]
+  const float* residual_hc;  // [rows][4][n_embd]
+  const float* norm_w;       // [n_embd]
+  float* split;              // [rows][24]
+  float* out;                // [rows][n_embd]
+  float* norm_out;           // [rows][n_embd]
+  int32_t n_embd, rows, iters;
+  float eps, norm_eps;
+};
+
 // FFN residual merge (hc.rs:212-259): out[t][dst][i] from the layer output,
 // the residual streams and the token's split row.
 struct HcExpandArgs {

@@ -252,10 +252,20 @@ template <bool kCoh>
 __device__ __forceinline__ void role_router_logits(const RouterLogitsArgs& a, int bx, uint8_t* smem) {
   const int row = bx % a.E, t0 = (bx / a.E) * 8, tx = threadIdx.x;
   const int nt = min(8, a.T - t0);
-  const int d = a.d;  // d % 256 == 0 and d <= 8192 checked on the host
+  const int d = a.d;  // d % 256 == 0 checked on the host
   const int nb = d >> 8;
   float (*part)[256] = (float (*)[256])smem;
   const uint16_t* wr = a.w + (size_t)row * d + tx;
+  if (nb > 32) {
+    // wide rows (the HC mix, d = 4 x 4096): the same per-thread order, one
+    // element at a time
+    for (int t = 0; t < nt; t++) {
+      const float* xr = a.x + (size_t)(t0 + t) * d + tx;
+      float acc = 0.0f;
+      for (int j = 0; j < nb; j++) acc = acc + f16_to_f32_ftz(wr[256 * j]) * xr[256 * j];
+      part[t][tx] = acc;
+    }
+  } else {
   uint32_t wh[32];
   float xv[32];
   {
@@ -282,6 +292,7 @@ __device__ __forceinline__ void role_router_logits(const RouterLogitsArgs& a, in
       acc = (j < nb) ? acc + pr : acc;
     }
     part[t][tx] = acc;
+  }
   }
   __syncthreads();
   // halving tree: levels 128 and 64 cross waves (LDS), levels 32..1 inside
@@ -2085,6 +2096,116 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_moe_sum(const MoeSumArgs
   float acc = 0.0f;
   for (int s = 0; s < a.k; s++) acc += a.down[(tok * a.k + s) * a.d + row];
   a.out[i] = acc;
+}
+
+// norm.rs:14-63: thread tx sums the squares of elements tx, tx + 256, ...,
+// the 128..1 halving tree in LDS, then every element times
+// 1 / sqrt(sum / n + eps).
+extern "C" __global__ __launch_bounds__(256) void dsmoe_rms_norm_plain(const RmsNormArgs a) {
+  __shared__ float part[256];
+  const int row = blockIdx.x, tx = threadIdx.x;
+  const float* x = a.x + (size_t)row * a.n;
+  float s = 0.0f;
+  for (int i = tx; i < a.n; i += 256) s = s + x[i] * x[i];
+  part[tx] = s;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (tx < st) part[tx] = part[tx] + part[tx + st];
+    __syncthreads();
+  }
+  const float scale = 1.0f / __builtin_sqrtf(part[0] / (float)a.n + a.eps);
+  for (int i = tx; i < a.n; i += 256) a.out[(size_t)row * a.n + i] = x[i] * scale;
+}
+
+// hc4_split_one (hc.rs:17-99) on one thread: pre weights, post weights and
+// the Sinkhorn-normalised 4x4 comb of one row.
+__device__ void hc4_split(const float* mix, const float* scale, const float* base, int iters, float eps,
+                          float* out) {
+  for (int i = 0; i < 4; i++) {
+    const float z = mix[i] * scale[0] + base[i];
+    out[i] = 1.0f / (1.0f + expf_dsm(-z)) + eps;
+  }
+  for (int i = 0; i < 4; i++) {
+    const float z = mix[4 + i] * scale[1] + base[4 + i];
+    out[4 + i] = 2.0f / (1.0f + expf_dsm(-z));
+  }
+  float c[16];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int col = 0; col < 4; col++) {
+      const float v = mix[8 + r * 4 + col] * scale[2] + base[8 + r * 4 + col];
+      c[r * 4 + col] = v;
+      if (v > m) m = v;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int col = 0; col < 4; col++) {
+      const float v = expf_dsm(c[r * 4 + col] - m);
+      c[r * 4 + col] = v;
+      s = s + v;
+    }
+#pragma unroll
+    for (int col = 0; col < 4; col++) c[r * 4 + col] = c[r * 4 + col] / s + eps;
+  }
+  auto cols = [&]() {
+#pragma unroll
+    for (int col = 0; col < 4; col++) {
+      float s = eps;
+#pragma unroll
+      for (int r = 0; r < 4; r++) s = s + c[r * 4 + col];
+#pragma unroll
+      for (int r = 0; r < 4; r++) c[r * 4 + col] = c[r * 4 + col] / s;
+    }
+  };
+  cols();
+  for (int it = 1; it < iters; it++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float s = eps;
+#pragma unroll
+      for (int col = 0; col < 4; col++) s = s + c[r * 4 + col];
+#pragma unroll
+      for (int col = 0; col < 4; col++) c[r * 4 + col] = c[r * 4 + col] / s;
+    }
+    cols();
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i++) out[8 + i] = c[i];
+}
+
+// hc.rs:313-398 (n_hc = 4): thread 0 writes the row's split, then thread tx
+// forms out[i] = sum_h residual[h][i] * pre[h] for i = tx, tx + 256, ... and
+// its squares, the 128..1 halving tree gives the norm, and
+// norm_out[i] = out[i] * norm_scale * norm_w[i].
+extern "C" __global__ __launch_bounds__(256) void dsmoe_hc_split_norm(const HcSplitNormArgs a) {
+  __shared__ float part[256];
+  __shared__ float sp[24];
+  const int t = blockIdx.x, tx = threadIdx.x, n = a.n_embd;
+  if (tx == 0) {
+    hc4_split(a.mix + (size_t)t * 24, a.scale, a.base, a.iters, a.eps, sp);
+    for (int i = 0; i < 24; i++) a.split[(size_t)t * 24 + i] = sp[i];
+  }
+  __syncthreads();
+  const float* res = a.residual_hc + (size_t)t * 4 * n;
+  float* o = a.out + (size_t)t * n;
+  float s = 0.0f;
+  for (int i = tx; i < n; i += 256) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 4; h++) acc = acc + res[(size_t)h * n + i] * sp[h];
+    o[i] = acc;
+    s = s + acc * acc;
+  }
+  part[tx] = s;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (tx < st) part[tx] = part[tx] + part[tx + st];
+    __syncthreads();
+  }
+  const float ns = 1.0f / __builtin_sqrtf(part[0] / (float)n + a.norm_eps);
+  for (int i = tx; i < n; i += 256) a.norm_out[(size_t)t * n + i] = o[i] * ns * a.norm_w[i];
 }
 
 // hc.rs:212-259.  One thread per output element, or per four consecutive

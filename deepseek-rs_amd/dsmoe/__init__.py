@@ -33,7 +33,7 @@ EXPORTED = [
     "dsmoe_q8_0_gemm",
     "dsmoe_gguf_open", "dsmoe_gguf_close", "dsmoe_gguf_tensor_count", "dsmoe_gguf_data_offset", "dsmoe_gguf_tensor_at",
     "dsmoe_gguf_find", "dsmoe_gguf_kv_u32", "dsmoe_gguf_kv_i32_array", "dsmoe_gguf_moe_layer",
-    "dsmoe_router_select_hash", "dsmoe_set_hash_routing",
+    "dsmoe_router_select_hash", "dsmoe_set_hash_routing", "dsmoe_rms_norm_plain", "dsmoe_hc_split_norm",
 ]
 GROUPED_TILE_M = 64  # DSMOE_GROUPED_TILE_M
 STAGE_COUNT = 9
@@ -81,6 +81,8 @@ def lib():
         "dsmoe_down_em": ([vp] * 8 + [i32, i32, i32, i32, i32, vp], i32),
         "dsmoe_router_select_hash": ([ctypes.POINTER(Config), vp, vp, i32, vp, i32, i32, vp, vp, vp, vp], i32),
         "dsmoe_set_hash_routing": ([vp, vp, i32, vp], i32),
+        "dsmoe_rms_norm_plain": ([vp, vp, i32, i32, f32, vp], i32),
+        "dsmoe_hc_split_norm": ([vp] * 8 + [i32, i32, i32, i32, f32, f32, vp], i32),
         "dsmoe_probe": ([i32, vp, ctypes.c_size_t, ctypes.c_int64, vp, vp], i32),
         "dsmoe_hc_expand": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp], i32),
         "dsmoe_forward_noalloc": ([ctypes.POINTER(Config), ctypes.POINTER(Weights), vp, i32, vp, vp, vp, vp, vp], i32),
@@ -333,6 +335,29 @@ def router_select_hash(cfg, logits, hash_table, hash_rows, tokens, token_scalar,
     c = cfg.c()
     check(lib().dsmoe_router_select_hash(ctypes.byref(c), _p(logits), _p(hash_table), hash_rows, _p(tokens),
                                          token_scalar, T, _p(probs), _p(selected), _p(weights), _stream(stream)))
+
+
+def rms_norm_plain(x, out, n, rows, eps, stream=None):
+    """rms_norm_plain (norm.rs:14-63)."""
+    check(lib().dsmoe_rms_norm_plain(_p(x), _p(out), n, rows, eps, _stream(stream)))
+
+
+def hc_split_norm(mix, scale, base, residual_hc, norm_w, split, out, norm_out, n_embd, n_rows, iters, eps, norm_eps,
+                  stream=None):
+    """hc_split_weighted_sum_norm_fused (hc.rs:313-398), n_hc = 4."""
+    check(lib().dsmoe_hc_split_norm(_p(mix), _p(scale), _p(base), _p(residual_hc), _p(norm_w), _p(split), _p(out),
+                                    _p(norm_out), n_embd, 4, n_rows, iters, eps, norm_eps, _stream(stream)))
+
+
+def hc_ffn_prenorm(hc, w_fn_f16, scale, base, norm_w, flat, mix, split, cur, norm, n_embd, T, iters=20, eps=1e-6,
+                   norm_eps=1e-6, stream=None):
+    """The FFN pre-norm chain of session.rs:1830-1892 for T rows of HC
+    residual streams hc [T][4][n_embd]: rms_norm_plain -> matmul_f16 (24
+    mix values per row) -> hc_split_weighted_sum_norm_fused; `norm` is the
+    layer input."""
+    rms_norm_plain(hc, flat, 4 * n_embd, T, norm_eps, stream)
+    router_logits(w_fn_f16, flat, mix, 4 * n_embd, 24, T, stream)
+    hc_split_norm(mix, scale, base, hc, norm_w, split, cur, norm, n_embd, T, iters, eps, norm_eps, stream)
 
 
 def probe(kind, src, nbytes, iters, sink, stream=None):

@@ -157,7 +157,8 @@ int dsmoe_profile_read(dsmoe_ctx* ctx, double* total_ms, int64_t* launches, int3
 /* Per-kernel entry points (the reference launch surface)                 */
 /* --------------------------------------------------------------------- */
 /* matmul_f16 (engine/src/kernels/matmul.rs:57-105): out[t][e] = sum_i
- * f16(w[e][i]) x[t][i], 256 strided partials + halving tree. */
+ * f16(w[e][i]) x[t][i], 256 strided partials + halving tree; d a multiple
+ * of 256, at most 65536. */
 int dsmoe_router_logits(const uint16_t* w, const float* x, float* out, int32_t d, int32_t E, int32_t T,
                         dsmoe_stream_t stream);
 
@@ -269,6 +270,24 @@ int dsmoe_probe(int32_t kind, const void* src, size_t bytes, int64_t iters, floa
 int dsmoe_router_select_hash(const dsmoe_config* cfg, const float* logits, const int32_t* hash, int32_t hash_rows,
                              const int32_t* tokens, int32_t token_scalar, int32_t T, float* probs,
                              int32_t* selected, float* weights, dsmoe_stream_t stream);
+
+/* The HC FFN pre-norm that produces the layer's input (session.rs:1830-1892):
+ * rms_norm_plain of the HC residual streams (engine/src/kernels/norm.rs:14-63),
+ * hc_mix = dsmoe_router_logits of it with the [24][n_hc * n_embd] f16
+ * hc_ffn_fn matrix (matmul_f16), then dsmoe_hc_split_norm. */
+/* rms_norm_plain: out[r][i] = x[r][i] * 1 / sqrt(sum of squares / n + eps),
+ * the sum over 256 lane-strided partials and a halving tree. */
+int dsmoe_rms_norm_plain(const float* x, float* out, int32_t n, int32_t rows, float eps, dsmoe_stream_t stream);
+/* hc_split_weighted_sum_norm_fused (engine/src/kernels/hc.rs:313-398, with
+ * hc4_split_one :17-99), n_hc = 4: per row the 24-value split (pre =
+ * sigmoid + eps, post = 2 sigmoid, comb = row softmax + eps, column
+ * normalisation and sinkhorn_iters - 1 Sinkhorn rounds) into split[row],
+ * out = sum_h residual_hc[row][h] * pre[h] (ffn_cur) and norm_out = out *
+ * 1 / sqrt(mean square + norm_eps) * norm_w (ffn_norm, the input of
+ * dsmoe_forward).  The exponentials are this library's expf. */
+int dsmoe_hc_split_norm(const float* mix, const float* scale, const float* base, const float* residual_hc,
+                        const float* norm_w, float* split, float* out, float* norm_out, int32_t n_embd, int32_t n_hc,
+                        int32_t n_rows, int32_t sinkhorn_iters, float eps, float norm_eps, dsmoe_stream_t stream);
 
 /* hc_expand (engine/src/kernels/hc.rs:212-259), the FFN residual merge that
  * consumes the layer's outputs (session.rs:2157-2175: block_out =

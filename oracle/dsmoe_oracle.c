@@ -30,6 +30,11 @@
  *                                  out-of-range tokens and ids (moe.rs:92-109)
  *   or_dispatch                    numpy stable argsort; prefix sums
  *   or_moe_sum                     f32 values whose sum depends on the slot order
+ *   or_rms_norm_plain              float64 within f32 rounding; exact on dyadic rows with eps 0
+ *   or_hc4_split / or_hc_split_norm float64 restatement (sigmoid, softmax, Sinkhorn, weighted
+ *                                  sum, norm) within f32 rounding; the comb's column sums after
+ *                                  the last Sinkhorn round; exp bits as or_expf (parity unpinned
+ *                                  against the reference GPU's exp)
  *   or_hc_expand                   dyadic inputs (exact in f32) vs the float64 formula, with
  *                                  a non-symmetric comb; numpy f32 in the reference's order
  *   or_moe_forward                 float64 dequantise-then-GEMM closed form through the same
@@ -564,6 +569,106 @@ void or_moe_sum(const float* down, float* out, int d, int k, int T) {
       for (int s = 0; s < k; s++) acc += down[((size_t)t * k + s) * d + r];
       out[(size_t)t * d + r] = acc;
     }
+}
+
+/* rms_norm_plain (engine/src/kernels/norm.rs:14-63): 256 lane-strided sums
+ * of squares, the halving tree 128..1, scale = 1 / sqrt(sum / n + eps),
+ * out = x * scale. */
+void or_rms_norm_plain(const float* x, float* out, int n, int rows, float eps) {
+  for (int r = 0; r < rows; r++) {
+    const float* xr = x + (size_t)r * n;
+    float part[256];
+    for (int l = 0; l < 256; l++) {
+      float s = 0.0f;
+      for (int i = l; i < n; i += 256) s += xr[i] * xr[i];
+      part[l] = s;
+    }
+    for (int st = 128; st > 0; st >>= 1)
+      for (int l = 0; l < st; l++) part[l] += part[l + st];
+    const float scale = 1.0f / sqrtf(part[0] / (float)n + eps);
+    for (int i = 0; i < n; i++) out[(size_t)r * n + i] = xr[i] * scale;
+  }
+}
+
+/* hc4_split_one (engine/src/kernels/hc.rs:17-99): out[0..4) = sigmoid(mix *
+ * s0 + base) + eps, out[4..8) = 2 sigmoid(mix * s1 + base), out[8..24) =
+ * the 4x4 comb: row softmax of mix * s2 + base (+ eps), a column
+ * normalisation, then iters - 1 Sinkhorn rounds (rows, then columns; every
+ * sum starts at eps). */
+void or_hc4_split(const float* mix, const float* scale, const float* base, int iters, float eps, float* out) {
+  for (int i = 0; i < 4; i++) {
+    const float z = mix[i] * scale[0] + base[i];
+    out[i] = 1.0f / (1.0f + or_expf(-z)) + eps;
+  }
+  for (int i = 0; i < 4; i++) {
+    const float z = mix[4 + i] * scale[1] + base[4 + i];
+    out[4 + i] = 2.0f / (1.0f + or_expf(-z));
+  }
+  float c[16];
+  for (int r = 0; r < 4; r++) {
+    float m = -INFINITY;
+    for (int col = 0; col < 4; col++) {
+      const float v = mix[8 + r * 4 + col] * scale[2] + base[8 + r * 4 + col];
+      c[r * 4 + col] = v;
+      if (v > m) m = v;
+    }
+    float s = 0.0f;
+    for (int col = 0; col < 4; col++) {
+      const float v = or_expf(c[r * 4 + col] - m);
+      c[r * 4 + col] = v;
+      s += v;
+    }
+    for (int col = 0; col < 4; col++) c[r * 4 + col] = c[r * 4 + col] / s + eps;
+  }
+  for (int col = 0; col < 4; col++) {
+    float s = eps;
+    for (int r = 0; r < 4; r++) s += c[r * 4 + col];
+    for (int r = 0; r < 4; r++) c[r * 4 + col] /= s;
+  }
+  for (int it = 1; it < iters; it++) {
+    for (int r = 0; r < 4; r++) {
+      float s = eps;
+      for (int col = 0; col < 4; col++) s += c[r * 4 + col];
+      for (int col = 0; col < 4; col++) c[r * 4 + col] /= s;
+    }
+    for (int col = 0; col < 4; col++) {
+      float s = eps;
+      for (int r = 0; r < 4; r++) s += c[r * 4 + col];
+      for (int r = 0; r < 4; r++) c[r * 4 + col] /= s;
+    }
+  }
+  for (int i = 0; i < 16; i++) out[8 + i] = c[i];
+}
+
+/* hc_split_weighted_sum_norm_fused (engine/src/kernels/hc.rs:313-398), n_hc
+ * = 4, a 256-thread row: the row's split (24 values, written to split),
+ * out[i] = sum over h in order of residual[h][i] * pre[h], its sum of squares
+ * over 256 lane-strided partials and the halving tree 128..1, then
+ * norm_out[i] = out[i] * (1 / sqrt(sumsq / n + norm_eps)) * norm_w[i]. */
+void or_hc_split_norm(const float* mix, const float* scale, const float* base, const float* residual_hc,
+                      const float* norm_w, float* split, float* out, float* norm_out, int n_embd, int n_rows,
+                      int iters, float eps, float norm_eps) {
+  for (int t = 0; t < n_rows; t++) {
+    float* sp = split + (size_t)t * 24;
+    or_hc4_split(mix + (size_t)t * 24, scale, base, iters, eps, sp);
+    const float* res = residual_hc + (size_t)t * 4 * n_embd;
+    float* o = out + (size_t)t * n_embd;
+    float part[256];
+    for (int l = 0; l < 256; l++) {
+      float s = 0.0f;
+      for (int i = l; i < n_embd; i += 256) {
+        float acc = 0.0f;
+        for (int h = 0; h < 4; h++) acc += res[(size_t)h * n_embd + i] * sp[h];
+        o[i] = acc;
+        s += acc * acc;
+      }
+      part[l] = s;
+    }
+    for (int st = 128; st > 0; st >>= 1)
+      for (int l = 0; l < st; l++) part[l] += part[l + st];
+    const float ns = 1.0f / sqrtf(part[0] / (float)n_embd + norm_eps);
+    for (int i = 0; i < n_embd; i++) norm_out[(size_t)t * n_embd + i] = o[i] * ns * norm_w[i];
+  }
 }
 
 /* hc_expand (engine/src/kernels/hc.rs:212-259): the FFN residual merge

@@ -71,6 +71,11 @@ void or_gate_up_mid(const uint8_t* gate, const uint8_t* up, const uint8_t* xq,
 void or_down(const uint8_t* down, const uint8_t* midq, const int32_t* selected,
              float* down_out, int d, int I, int T, int k, int nthreads);
 void or_moe_sum(const float* down, float* out, int d, int k, int T);
+void or_rms_norm_plain(const float* x, float* out, int n, int rows, float eps);
+void or_hc4_split(const float* mix, const float* scale, const float* base, int iters, float eps, float* out);
+void or_hc_split_norm(const float* mix, const float* scale, const float* base, const float* residual_hc,
+                      const float* norm_w, float* split, float* out, float* norm_out, int n_embd, int n_rows,
+                      int iters, float eps, float norm_eps);
 void or_hc_expand(const float* block_out, const float* block_add, const float* residual_hc, const float* split,
                   float* out_hc, int n_embd, int n_hc, int n_tokens, int mix_hc, int has_add);
 

@@ -62,6 +62,9 @@ def load():
         "or_down": ([vp, vp, vp, vp, i32, i32, i32, i32, i32], None),
         "or_moe_sum": ([vp, vp, i32, i32, i32], None),
         "or_router_select_hash": ([vp, vp, vp, i32, vp, i32, i32, vp, vp, vp], None),
+        "or_rms_norm_plain": ([vp, vp, i32, i32, f32], None),
+        "or_hc4_split": ([vp, vp, vp, i32, f32, vp], None),
+        "or_hc_split_norm": ([vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, f32, f32], None),
         "or_hc_expand": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, i32], None),
         "or_dispatch": ([vp, i32, i32, i32, vp, vp, vp, vp, vp, vp], None),
         "or_moe_forward": ([ctypes.POINTER(OrConfig), vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, vp, vp, vp, i32], i32),
@@ -131,6 +134,29 @@ def dispatch(sel, E, block_m):
     load().or_dispatch(P(np.ascontiguousarray(sel, np.int32)), pairs, E, block_m, P(counts), P(offsets), P(sp),
                        P(to), P(te), P(ts))
     return counts, offsets, sp[:pairs], to, te[:to[E]], ts[:to[E]]
+
+
+def rms_norm_plain(x, n, rows, eps):
+    out = np.zeros(rows * n, np.float32)
+    load().or_rms_norm_plain(P(np.ascontiguousarray(x, np.float32)), P(out), n, rows, eps)
+    return out.reshape(rows, n)
+
+
+def hc4_split(mix, scale, base, iters, eps):
+    out = np.zeros(24, np.float32)
+    f = lambda a: np.ascontiguousarray(a, np.float32)
+    load().or_hc4_split(P(f(mix)), P(f(scale)), P(f(base)), iters, eps, P(out))
+    return out
+
+
+def hc_split_norm(mix, scale, base, residual_hc, norm_w, n_embd, n_rows, iters, eps, norm_eps):
+    f = lambda a: np.ascontiguousarray(a, np.float32)
+    split = np.zeros(n_rows * 24, np.float32)
+    out = np.zeros(n_rows * n_embd, np.float32)
+    nout = np.zeros(n_rows * n_embd, np.float32)
+    load().or_hc_split_norm(P(f(mix)), P(f(scale)), P(f(base)), P(f(residual_hc)), P(f(norm_w)), P(split), P(out),
+                            P(nout), n_embd, n_rows, iters, eps, norm_eps)
+    return split.reshape(n_rows, 24), out.reshape(n_rows, n_embd), nout.reshape(n_rows, n_embd)
 
 
 def hc_expand(block_out, block_add, residual_hc, split, n_embd, n_hc, T, mix_hc, has_add):

@@ -764,3 +764,81 @@ def test_layer_with_hash_routing(gpu, T):
     lay.forward(w, x, so, ro, sel, wt)  # back to top-k
     torch.cuda.synchronize()
     lay.close()
+
+
+# ---------------------------------------------------------------- HC FFN pre-norm
+@pytest.mark.parametrize("n,rows,eps", [(256, 1, 1e-5), (128, 1, 1e-5), (16384, 3, 1e-6), (1000, 2, 1e-6)])
+def test_rms_norm_plain_bitexact(gpu, n, rows, eps):
+    """rms_norm_plain (norm.rs:14-63) against the oracle bit for bit, with
+    the reference's own checks (kernels_smoke.rs:306-392) on all-equal rows."""
+    import torch
+    say(f"rms_norm_plain n={n} rows={rows}")
+    rng = np.random.default_rng(n)
+    x = rng.normal(0, 2, (rows, n)).astype(np.float32)
+    out = torch.full((rows, n), float("nan"), device=gpu)
+    dsmoe.rms_norm_plain(torch.from_numpy(x).to(gpu), out, n, rows, eps)
+    torch.cuda.synchronize()
+    assert bits_equal(np_(out), O.rms_norm_plain(x, n, rows, eps))
+    if n in (128, 256):
+        one = torch.full((1, n), 2.0, device=gpu)
+        three = torch.full((1, n), 3.0, device=gpu)
+        o1, o3 = torch.empty_like(one), torch.empty_like(three)
+        dsmoe.rms_norm_plain(one, o1, n, 1, eps)
+        dsmoe.rms_norm_plain(three, o3, n, 1, eps)
+        torch.cuda.synchronize()
+        assert abs(float(o1.pow(2).mean().sqrt()) - 1.0) < 1e-3 and bool((o1 == o1[0, 0]).all())
+        assert abs(float(o1[0, 0]) - float(o3[0, 0])) < 1e-4
+
+
+@pytest.mark.parametrize("n,T,iters", [(4096, 1, 20), (4096, 5, 20), (1000, 2, 1), (7168, 3, 3)])
+def test_hc_split_norm_bitexact(gpu, n, T, iters):
+    """hc_split_weighted_sum_norm_fused (hc.rs:313-398): split, ffn_cur and
+    ffn_norm against the oracle bit for bit."""
+    import torch
+    say(f"hc_split_norm n={n} T={T} iters={iters}")
+    rng = np.random.default_rng(n + T)
+    mix = rng.normal(0, 1, (T, 24)).astype(np.float32)
+    scale = np.array([0.5, 1.0, 1.5], np.float32)
+    base = rng.normal(0, 0.3, 24).astype(np.float32)
+    res = rng.normal(0, 1, (T, 4, n)).astype(np.float32)
+    nw = rng.normal(1, 0.1, n).astype(np.float32)
+    d = lambda a: torch.from_numpy(a).to(gpu)
+    split = torch.full((T, 24), float("nan"), device=gpu)
+    cur, norm = (torch.full((T, n), float("nan"), device=gpu) for _ in range(2))
+    dsmoe.hc_split_norm(d(mix), d(scale), d(base), d(res), d(nw), split, cur, norm, n, T, iters, 1e-6, 1e-6)
+    torch.cuda.synchronize()
+    ws, wc, wn = O.hc_split_norm(mix, scale, base, res, nw, n, T, iters, 1e-6, 1e-6)
+    assert bits_equal(np_(split), ws)
+    assert bits_equal(np_(cur), wc)
+    assert bits_equal(np_(norm), wn)
+
+
+def test_hc_ffn_prenorm_chain(gpu):
+    """The FFN pre-norm of session.rs:1830-1892 at the reference's shape
+    (n_embd 4096, HC_DIM 16384, 24 mix values): rms_norm_plain ->
+    router_logits (matmul_f16, d = 16384 on the wide-row path) ->
+    hc_split_norm, each stage bit-equal to the oracle on the previous stage's
+    oracle output, and the layer input `norm` bit-equal end to end."""
+    import torch
+    n, T = 4096, 2
+    say(f"hc_ffn_prenorm n={n} T={T}")
+    rng = np.random.default_rng(11)
+    hc = rng.normal(0, 1, (T, 4, n)).astype(np.float32)
+    wfn = (rng.normal(0, 0.02, (24, 4 * n)).astype(np.float16)).view(np.uint16)
+    scale = np.array([0.5, 1.0, 1.5], np.float32)
+    base = rng.normal(0, 0.3, 24).astype(np.float32)
+    nw = rng.normal(1, 0.1, n).astype(np.float32)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    flat = torch.empty(T, 4 * n, device=gpu)
+    mix = torch.empty(T, 24, device=gpu)
+    split = torch.empty(T, 24, device=gpu)
+    cur, norm = torch.empty(T, n, device=gpu), torch.empty(T, n, device=gpu)
+    wdev = torch.from_numpy(wfn.view(np.int16)).to(gpu)
+    dsmoe.hc_ffn_prenorm(d(hc), wdev, d(scale), d(base), d(nw), flat, mix, split, cur, norm, n, T)
+    torch.cuda.synchronize()
+    f = O.rms_norm_plain(hc.reshape(T, 4 * n), 4 * n, T, 1e-6)
+    assert bits_equal(np_(flat), f)
+    m = O.router_logits(wfn, f, 4 * n, 24, T)
+    assert bits_equal(np_(mix), m)
+    ws, wc, wn = O.hc_split_norm(m, scale, base, hc, nw, n, T, 20, 1e-6, 1e-6)
+    assert bits_equal(np_(split), ws) and bits_equal(np_(cur), wc) and bits_equal(np_(norm), wn)

@@ -586,3 +586,101 @@ def test_router_select_hash_restated(oracle):
     assert np.allclose(w[ok].sum(1), 2.5, rtol=1e-5)
     _, sel2, _ = oracle_ref.router_select_hash(cfg, logits, table, rows, None, 7, T)
     assert (sel2 == table[7]).all()
+
+
+# ---------------------------------------------------------------- HC FFN pre-norm
+def test_rms_norm_plain_reference_tests(oracle):
+    """engine/tests/kernels_smoke.rs:306-392: all-equal input gives
+    all-equal output of RMS 1 (n = 256, eps 1e-5), and 1.0 and 3.0 inputs
+    (n = 128) give the same output."""
+    out = oracle_ref.rms_norm_plain(np.full(256, 2.0), 256, 1, 1e-5)[0]
+    assert abs(math.sqrt(float(np.mean(out.astype(np.float64) ** 2))) - 1.0) < 1e-3
+    assert np.all(out == out[0])
+    a = oracle_ref.rms_norm_plain(np.full(128, 1.0), 128, 1, 1e-5)[0]
+    b = oracle_ref.rms_norm_plain(np.full(128, 3.0), 128, 1, 1e-5)[0]
+    assert abs(float(a[0]) - float(b[0])) < 1e-4
+
+
+def test_rms_norm_plain_exact_and_float64(oracle):
+    """eps = 0 and x = +-2 gives mean square 4, so every output is exactly
+    +-1 (a dropped 1/n or a sqrt of the sum fails); random rows are within
+    f32 rounding of the float64 formula, each row normalised by its own
+    mean square (n = 1000 is not a multiple of 256)."""
+    rng = np.random.default_rng(3)
+    x = np.where(rng.random(512) < 0.5, -2.0, 2.0).astype(np.float32)
+    assert np.array_equal(oracle_ref.rms_norm_plain(x, 512, 1, 0.0)[0], x / 2)
+    for n in (1000, 16384):
+        x = rng.normal(0, 3, (3, n)).astype(np.float32)
+        x[1] *= 100
+        got = oracle_ref.rms_norm_plain(x, n, 3, 1e-6).astype(np.float64)
+        x64 = x.astype(np.float64)
+        want = x64 / np.sqrt(np.mean(x64 ** 2, axis=1, keepdims=True) + 1e-6)
+        assert np.max(np.abs(got - want)) < 2e-6 * np.max(np.abs(want))
+
+
+def _sinkhorn64(logits, iters, eps):
+    """Float64 hc4_split_one comb (hc.rs:40-99): row softmax + eps, a
+    column normalisation, then iters - 1 rounds of rows then columns, every
+    normaliser starting at eps."""
+    c = np.exp(logits - logits.max(axis=1, keepdims=True))
+    c = c / c.sum(axis=1, keepdims=True) + eps
+    c = c / (eps + c.sum(axis=0, keepdims=True))
+    for _ in range(iters - 1):
+        c = c / (eps + c.sum(axis=1, keepdims=True))
+        c = c / (eps + c.sum(axis=0, keepdims=True))
+    return c
+
+
+@pytest.mark.parametrize("iters", [1, 2, 20])
+def test_hc4_split_float64(oracle, iters):
+    """pre = sigmoid + eps, post = 2 sigmoid and the Sinkhorn comb within
+    f32 rounding of float64; after 20 iterations the comb is doubly
+    stochastic to 1e-5; scale = 0 makes the split a function of base alone;
+    swapping two rows of comb logits swaps the comb's rows."""
+    rng = np.random.default_rng(iters)
+    eps = 1e-6
+    mix = rng.normal(0, 1, 24).astype(np.float32)
+    scale = np.array([0.7, 1.3, 2.1], np.float32)
+    base = rng.normal(0, 0.5, 24).astype(np.float32)
+    got = oracle_ref.hc4_split(mix, scale, base, iters, eps).astype(np.float64)
+    z = mix.astype(np.float64) * np.repeat(scale.astype(np.float64), [4, 4, 16]) + base
+    sig = 1 / (1 + np.exp(-z[:8]))
+    assert np.max(np.abs(got[:4] - (sig[:4] + eps))) < 1e-6
+    assert np.max(np.abs(got[4:8] - 2 * sig[4:8])) < 2e-6
+    comb = _sinkhorn64(z[8:].reshape(4, 4), iters, eps)
+    assert np.max(np.abs(got[8:].reshape(4, 4) - comb)) < 1e-5 * iters
+    if iters == 20:
+        cm = got[8:].reshape(4, 4)
+        assert np.max(np.abs(cm.sum(axis=0) - 1)) < 1e-5 and np.max(np.abs(cm.sum(axis=1) - 1)) < 1e-5
+    a = oracle_ref.hc4_split(mix, np.zeros(3, np.float32), base, iters, eps)
+    b = oracle_ref.hc4_split(rng.normal(0, 1, 24), np.zeros(3, np.float32), base, iters, eps)
+    assert np.array_equal(a, b)
+    sw = mix.copy()
+    sw[8:12], sw[12:16] = mix[12:16], mix[8:12]
+    bsw = base.copy()
+    bsw[8:12], bsw[12:16] = base[12:16], base[8:12]
+    c1 = oracle_ref.hc4_split(mix, scale, base, iters, eps)[8:].reshape(4, 4)
+    c2 = oracle_ref.hc4_split(sw, scale, bsw, iters, eps)[8:].reshape(4, 4)
+    assert np.max(np.abs(c1[[1, 0, 2, 3]] - c2)) < 1e-6
+
+
+def test_hc_split_norm_float64(oracle):
+    """hc_split_weighted_sum_norm_fused (hc.rs:313-398): split rows equal
+    hc4_split of each mix row; ffn_cur = sum_h residual[h] * pre[h] within
+    f32 rounding of float64 (weights pre, not post: the residual rows are
+    scaled so that a swap changes the result); norm_out = ffn_cur times
+    its rms scale times norm_w."""
+    rng = np.random.default_rng(5)
+    T, n = 3, 1000
+    mix = rng.normal(0, 1, (T, 24)).astype(np.float32)
+    scale = np.array([0.5, 1.0, 1.5], np.float32)
+    base = rng.normal(0, 0.3, 24).astype(np.float32)
+    res = (rng.normal(0, 1, (T, 4, n)) * np.array([1, 2, 3, 4])[None, :, None]).astype(np.float32)
+    nw = rng.normal(1, 0.1, n).astype(np.float32)
+    split, cur, nout = oracle_ref.hc_split_norm(mix, scale, base, res, nw, n, T, 20, 1e-6, 1e-6)
+    for t in range(T):
+        assert np.array_equal(split[t], oracle_ref.hc4_split(mix[t], scale, base, 20, 1e-6))
+        c64 = np.einsum("h,hi->i", split[t, :4].astype(np.float64), res[t].astype(np.float64))
+        assert np.max(np.abs(cur[t] - c64)) < 1e-5 * np.max(np.abs(c64))
+        n64 = c64 / np.sqrt(np.mean(c64 ** 2) + 1e-6) * nw
+        assert np.max(np.abs(nout[t] - n64)) < 2e-5 * np.max(np.abs(n64))
