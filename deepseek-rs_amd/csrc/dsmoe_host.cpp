@@ -181,8 +181,8 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // per CU (256 CUs).
 constexpr int kMinWgs = 512;
 constexpr int kDecodeMaxT = kMaxDecodeT;  // row-streaming (matvec) launches up to 8 tokens, batch paths above
-constexpr int kEmMaxLoad = 4;
-constexpr int kQ80MaxSplit = 8;  // class groups of a split shared-expert GEMM (up to 256 tokens)  // pairs per expert (on average) up to which batches run expert-major
+constexpr int kEmMaxLoad = 4;    // pairs per expert (on average) up to which batches run expert-major
+constexpr int kQ80MaxSplit = 8;  // class groups of a split shared-expert GEMM (up to 256 tokens)
 #ifdef DSM_PROBE
 // measurement builds only: launch-shape overrides from the environment
 int dsm_tune(const char* name, int def) {
@@ -232,18 +232,6 @@ size_t gate_up_rows_lds(int nb) { return 3072 + (size_t)align_up(nb, 4) * 4 + (s
 size_t q80_rows_lds(int nb) { return (size_t)align_up(nb, 4) * 4 + (size_t)nb * 32 + 32; }
 // Experts per lane of the one-wave selection (E = 64 * P, groups of whole
 // lane blocks of 1..16 lanes), or 0 when the selection needs the LDS form.
-int select_wave_p(const dsmoe_config& cf) {
-  const int E = cf.n_expert, G = cf.n_group > 1 ? cf.n_group : 1;
-  for (int P : {1, 2, 4}) {
-    if (E != 64 * P) continue;
-    if (G == 1) return P;
-    const int gsz = E / G;
-    if (gsz % P) return 0;
-    const int lpg = gsz / P;
-    return (lpg == 1 || lpg == 2 || lpg == 4 || lpg == 8 || lpg == 16) ? P : 0;
-  }
-  return 0;
-}
 // Expert-major launches (dsmoe_up_em / dsmoe_dn_em): shapes they take.  The
 // gate/up workgroup stages up to kEmPairs activations in LDS (at most 64 KB).
 size_t gate_up_em_lds(int nb, int np = kEmPairs) { return 3072 + (size_t)np * nb * 272; }
@@ -259,7 +247,7 @@ size_t down_lds(int K, int nb, int R) {
          (size_t)K * R * 4;
 }
 size_t q80_lds(int nb, int nmat, int R) { return (size_t)align_up(nb, 4) * 4 + (size_t)nb * 32 + (size_t)nmat * R * nb * 4; }
-size_t select_lds(int E) { return (size_t)E * 16 + 64 * 24 + 32 * 4; }
+size_t select_lds(int E) { return (size_t)E * 20 + 128 * 4 + 64 * 4 + 32 * 8; }
 size_t router_lds(int) { return 8 * 256 * 4; }
 
 int validate_cfg(const dsmoe_config* c) {
@@ -1008,6 +996,10 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // stream their weights once per chunk of em_pairs() pairs
   // (expert-major matvec) instead of dequantizing them into MFMA tiles.
   const bool em = grouped && (int64_t)P <= (int64_t)kEmMaxLoad * E && em_fits(cf);
+  // In the row-streaming path the selection needs no launch of its own:
+  // every routed gate/up workgroup runs it for its token.
+  const bool up_rows = !grouped && up_rows_fits(d) && (cf.shared_fmt != 0 || q80_rows_fits(d));
+  const bool fuse_sel = up_rows && !c->hash && DSM_TUNE("DSM_FUSE_SEL", 1);
   // 1. router logits + Q8_K(x) + Q8_0(x)          (session.rs:1894-1909, 1991-2008, 2062-2073)
   {
     StageScope sc(c, DSMOE_STAGE_PREP, stream);
@@ -1017,11 +1009,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     DSM_TRY(prep_impl(&r, &q8k, cf.shared_fmt == 0 ? &q80 : nullptr, stream));
   }
   // 2. routing                                     (session.rs:2010-2058)
-  // In the row-streaming path every routed gate/up workgroup runs the
-  // one-wave selection itself (no launch of its own).
-  const bool up_rows = !grouped && up_rows_fits(d) && (cf.shared_fmt != 0 || q80_rows_fits(d));
-  const int fuse_p = up_rows && !c->hash ? select_wave_p(cf) : 0;
-  if (!fuse_p) {
+  if (!fuse_sel) {
     StageScope sc(c, DSMOE_STAGE_SELECT, stream);
     if (c->hash)  // hash routing (moe.rs:92-109): the token ids pick the experts
       DSM_TRY(dsmoe_router_select_hash(&cf, c->logits, c->hash, c->hash_rows, c->hash_tokens, 0, T, nullptr, sel,
@@ -1042,8 +1030,8 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     UpArgs a{};
     Shape s1, s2{0, 64, 0};
     const int mb = 256;
-    if (fuse_p) {
-      a.fuse_sel = fuse_p;
+    if (fuse_sel) {
+      a.fuse_sel = 1;
       a.sel = RouterSelectArgs{c->logits, cf.has_bias ? w->bias : nullptr, nullptr, sel, wts, T, E, K,
                                cf.n_group > 1 ? cf.n_group : 1, cf.topk_group, cf.has_bias ? 1 : 0, cf.route_scale};
     }
@@ -1053,6 +1041,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     a.gu_tiles = s1.tiles;
     a.gu_work = grouped ? 0 : P;
     size_t lds = up_rows ? gate_up_rows_lds(nb) : gate_up_lds(nb, s1.R);
+    if (fuse_sel) lds = std::max(lds, select_lds(E));
     if (em) {
       StageScope sg(c, DSMOE_STAGE_GU_GROUPED, stream);
       DSM_TRY(dsmoe_gate_up_mid_em(w->gate, w->up, c->xq8k, c->g_sorted, c->g_offsets, c->g_tile_offsets,

@@ -127,7 +127,7 @@ struct UpArgs {
   int32_t sh_tiles, sh_work;
   int32_t sh_fmt;
   RouterSelectArgs sel;       // dsmoe_up_rows with fuse_sel: every routed workgroup runs the selection itself
-  int32_t fuse_sel = 0;       // 0, or P = E / 64 (1, 2, 4): experts per lane of the one-wave selection
+  int32_t fuse_sel = 0;       // 1: the routed workgroups run the selection (T <= 8)
   // dsmoe_up_rows with fuse_midq: the workgroup that completes the 256 rows
   // of a (pair, block) writes its Q8_K (midq), the one that completes a
   // token's 256-row group of the Q8_0 shared mid writes its 8 Q8_0 blocks

@@ -671,62 +671,22 @@ __device__ __forceinline__ void role_gate_up(const GateUpArgs& a, int tile, int 
 // Router selection: moe.rs:177-287 (router_select_parallel) generalised to E
 // experts, top-k, route_scale and group-limited selection.  One 256-thread
 // workgroup per token.  The reference's insertion sort keeps the k best by
-// (score desc, index asc) among scores > -inf; here every eligible expert
-// computes its rank under that order (a 64-bit key: ordered score bits, then
-// the complemented index) and the experts with rank < k place themselves.
-// Group score = best + second best biased score in the group.
+// (score desc, index asc) among scores > -inf; here every expert has a 64-bit
+// key (ordered score bits, then the complemented index) and places itself by
+// its rank under that order.  Group score = best + second-best biased score
+// in the group.  An expert ranks below k overall only if it ranks below k in
+// its group, so only each group's k best (its candidates) are ranked against
+// the candidates of the kept groups: 32 comparisons per expert inside an
+// 8 x 32 grouping, then 32 per candidate, no sequential arg-max rounds.
 // ---------------------------------------------------------------------------
 // LDS: select_lds(E) bytes; 256 threads.
-__device__ __forceinline__ size_t select_lds(int E) { return (size_t)E * 16 + 64 * 24 + 32 * 4; }
+__device__ __forceinline__ size_t select_lds(int E) { return (size_t)E * 20 + 128 * 4 + 64 * 4 + 32 * 8; }
 
-// Cross-lane moves inside one wavefront with DPP (no LDS round trip).
-// Partner of lane i for step m = 1, 2, 4, 8: i^1, i^2 (quad permutes), then
-// the mirror inside 8 and inside 16 lanes, which for values already uniform
-// over blocks of m lanes is the same as i^m.
-template <int kCtrl>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, kCtrl, 0xF, 0xF, false);
-}
-template <int kStep>
-__device__ __forceinline__ uint32_t partner_u32(uint32_t v) {
-  if constexpr (kStep == 1) return dpp_u32<0xB1>(v);   // quad_perm [1,0,3,2]
-  else if constexpr (kStep == 2) return dpp_u32<0x4E>(v);  // quad_perm [2,3,0,1]
-  else if constexpr (kStep == 4) return dpp_u32<0x141>(v); // row_half_mirror
-  else return dpp_u32<0x140>(v);                           // row_mirror
-}
-template <int kStep>
-__device__ __forceinline__ uint64_t partner_u64(uint64_t v) {
-  return ((uint64_t)partner_u32<kStep>((uint32_t)(v >> 32)) << 32) | partner_u32<kStep>((uint32_t)v);
-}
 __device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
 }
-// Wave-wide maximum of a 32-bit unsigned value (uniform result).
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  v = max(v, partner_u32<1>(v));
-  v = max(v, partner_u32<2>(v));
-  v = max(v, partner_u32<4>(v));
-  v = max(v, partner_u32<8>(v));
-  return max(max(readlane_u32(v, 0), readlane_u32(v, 16)), max(readlane_u32(v, 32), readlane_u32(v, 48)));
-}
-// Wave-wide maximum of a 64-bit key: the high words first, then the low
-// words of the lanes that hold the maximal high word.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
-  const uint32_t hi = wave_max_u32((uint32_t)(k >> 32));
-  const uint32_t lo = wave_max_u32((uint32_t)(k >> 32) == hi ? (uint32_t)k : 0u);
-  return ((uint64_t)hi << 32) | lo;
-}
-// Merge the top-2 keys (k1 >= k2) of this lane with the partner's.
-struct Top2 {
-  uint64_t k1, k2;
-};
-template <int kStep>
-__device__ __forceinline__ Top2 merge_top2(Top2 a) {
-  const uint64_t o1 = partner_u64<kStep>(a.k1), o2 = partner_u64<kStep>(a.k2);
-  const bool up = o1 > a.k1;
-  const uint64_t hi2 = a.k1 > o2 ? a.k1 : o2;
-  const uint64_t lo2 = o1 > a.k2 ? o1 : a.k2;
-  return Top2{up ? o1 : a.k1, up ? hi2 : lo2};
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  return ((uint64_t)readlane_u32((uint32_t)(v >> 32), l) << 32) | readlane_u32((uint32_t)v, l);
 }
 // Score back from the high half of a rank key (inverse of ord_f32).
 __device__ __forceinline__ float key_score(uint64_t k) {
@@ -734,112 +694,137 @@ __device__ __forceinline__ float key_score(uint64_t k) {
   return __builtin_bit_cast(float, (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
 }
 
-// The same selection on one wavefront, for E = 64 * P experts with lane l
-// holding experts l*P .. l*P+P-1 (groups of gsz experts are then gsz/P
-// adjacent lanes, at most 16).  Group scores merge per-lane top-2 keys over
-// the group's lanes; the top k are k rounds of a wave-wide maximum of the
-// keys.  No LDS and no barriers: the critical path of a decode step runs
-// through here.
-// With s_sel / s_w the k results also go to LDS (slot r at index r), and
-// `global` says whether they go to a.selected / a.weights.
-template <bool kCoh, int P>
-__device__ __forceinline__ void select_wave(const RouterSelectArgs& a, int t, int32_t* s_sel = nullptr,
+template <bool kCoh>
+__device__ __forceinline__ void role_select(const RouterSelectArgs& a, int t, uint8_t* smem, int32_t* s_sel = nullptr,
                                             float* s_w = nullptr, bool global = true) {
-  const int lane = threadIdx.x & 63;
-  const int E = a.E, K = a.k, G = a.n_group > 1 ? a.n_group : 1, gsz = E / G;
-  uint64_t key[P];
-  float pv[P];
-  float lg[P], bs[P];  // every load issued before the first use
-#pragma unroll
-  for (int i = 0; i < P; i++) {
-    lg[i] = ldc<kCoh>(a.logits + (size_t)t * E + lane * P + i);
-    bs[i] = a.has_bias ? a.bias[lane * P + i] : 0.0f;
+  const int E = a.E, K = a.k, G = a.n_group > 1 ? a.n_group : 1, gsz = E / G, Kc = min(K, gsz);
+  const int tid = threadIdx.x;
+  uint64_t* l_key = (uint64_t*)smem;  // [E]
+  uint64_t* l_cand = l_key + E;       // [G][Kc]: the Kc best keys of each group, by rank
+  float* l_p = (float*)(l_cand + E);  // [E]
+  float* l_gb = l_p + E;              // [64][2]: best and second-best score per group
+  int* l_keep = (int*)(l_gb + 128);   // [64]
+  int* l_sel = l_keep + 64;           // [32]
+  float* l_sp = (float*)(l_sel + 32); // [32]
+  // 1. probabilities and keys, one to four experts per thread
+  for (int e = tid; e < E; e += 256) {
+    const float pv = __builtin_sqrtf(softplus_dsm(ldc<kCoh>(a.logits + (size_t)t * E + e)));
+    const float sc = a.has_bias ? pv + a.bias[e] : pv;
+    l_p[e] = pv;
+    l_key[e] = sc > -__builtin_inff() ? (((uint64_t)ord_f32(sc) << 32) | (0xFFFFFFFFu - (uint32_t)e)) : 0ull;
+    if (a.probs) a.probs[(size_t)t * E + e] = pv;
   }
-#pragma unroll
-  for (int i = 0; i < P; i++) {
-    const int e = lane * P + i;
-    pv[i] = __builtin_sqrtf(softplus_dsm(lg[i]));
-    const float sc = a.has_bias ? pv[i] + bs[i] : pv[i];
-    key[i] = sc > -__builtin_inff() ? (((uint64_t)ord_f32(sc) << 32) | (0xFFFFFFFFu - (uint32_t)e)) : 0ull;
-    if (a.probs) a.probs[(size_t)t * E + e] = pv[i];
-  }
-  if (G > 1) {
-    // top-2 keys of this lane, then of the group's lanes
-    Top2 tp{0ull, 0ull};
-#pragma unroll
-    for (int i = 0; i < P; i++) {
-      const bool up = key[i] > tp.k1;
-      const uint64_t n2 = up ? tp.k1 : (key[i] > tp.k2 ? key[i] : tp.k2);
-      tp.k1 = up ? key[i] : tp.k1;
-      tp.k2 = n2;
-    }
-    const int lpg = gsz / P;
-    if (lpg > 1) tp = merge_top2<1>(tp);
-    if (lpg > 2) tp = merge_top2<2>(tp);
-    if (lpg > 4) tp = merge_top2<4>(tp);
-    if (lpg > 8) tp = merge_top2<8>(tp);
-    const float b1 = tp.k1 ? key_score(tp.k1) : -__builtin_inff();
-    const float b2 = tp.k2 ? key_score(tp.k2) : -__builtin_inff();
-    const int g = lane / lpg;
-    const float gs = gsz >= 2 ? b1 + b2 : b1;
-    const uint64_t gkey = gs > -__builtin_inff() ? (((uint64_t)ord_f32(gs) << 32) | (0xFFFFFFFFu - (uint32_t)g)) : 0ull;
+  if (tid < 128) l_gb[tid] = -__builtin_inff();
+  if (tid < 32) { l_sel[tid] = -1; l_sp[tid] = 0.0f; }
+  if (G > 1)
+    for (int i = tid; i < G * Kc; i += 256) l_cand[i] = 0ull;
+  __syncthreads();
+  // 2. rank of each expert inside its group: ranks 0 and 1 give the group
+  //    score, ranks below Kc are the group's candidates (with one group, the
+  //    rank is the slot)
+  for (int e = tid; e < E; e += 256) {
+    const uint64_t k0 = l_key[e];
+    if (!k0) continue;
+    const int g = e / gsz, base = g * gsz;
     int r = 0;
-    for (int g2 = 0; g2 < G; g2++) {
-      const uint64_t o = ((uint64_t)readlane_u32((uint32_t)(gkey >> 32), g2 * lpg) << 32) |
-                         readlane_u32((uint32_t)gkey, g2 * lpg);
-      r += o > gkey;
+#pragma unroll 8
+    for (int j = 0; j < gsz; j++) r += l_key[base + j] > k0;
+    if (G == 1) {
+      if (r < K) { l_sel[r] = e; l_sp[r] = l_p[e]; }
+      continue;
     }
-    if (!(gkey && r < a.topk_group)) {
-#pragma unroll
-      for (int i = 0; i < P; i++) key[i] = 0ull;
+    if (r < 2) l_gb[2 * g + r] = key_score(k0);
+    if (r < Kc) l_cand[g * Kc + r] = k0;
+  }
+  __syncthreads();
+  const int NC = G * Kc;  // candidate slots
+  int NS = 1;              // threads per candidate slot (a power of two)
+  while (NS * 2 * NC <= 256 && NS < 64) NS *= 2;
+  if (G > 1 && G * G <= 64) {
+    // 3. kept groups, all pairs at once: lane g * G + h of wave 0 compares
+    //    group h's key with group g's; the ballot's G bits of group g are its rank
+    auto gkey = [&](int g) -> uint64_t {
+      const float gs = gsz >= 2 ? l_gb[2 * g] + l_gb[2 * g + 1] : l_gb[2 * g];
+      return gs > -__builtin_inff() ? (((uint64_t)ord_f32(gs) << 32) | (0xFFFFFFFFu - (uint32_t)g)) : 0ull;
+    };
+    if (tid < 64) {
+      const int g = tid / G, h = tid - g * G;
+      const bool act = tid < G * G;
+      const uint64_t kg = act ? gkey(g) : 0ull, kh = act ? gkey(h) : 0ull;
+      const uint64_t m = __ballot(act && kh > kg);
+      const bool keep = act && h == 0 && kg && __popcll((m >> (g * G)) & ((1ull << G) - 1)) < a.topk_group;
+      const uint64_t km = __ballot(keep);  // bit g * G for a kept group g
+      // the candidates of the other groups drop out
+      for (int i = tid; i < NC; i += 64)
+        if (!((km >> ((i / Kc) * G)) & 1)) l_cand[i] = 0ull;
     }
-  }
-  // k rounds of arg-max; lane r keeps slot r
-  int my_sel = -1;
-  float my_p = 0.0f;
-  for (int r = 0; r < K; r++) {
-    uint64_t m = 0;
-#pragma unroll
-    for (int i = 0; i < P; i++) m = key[i] > m ? key[i] : m;
-    const uint64_t wm = wave_max_u64(m);
-    if (wm == 0ull) break;  // no eligible expert left: slots r.. stay -1
-    const int e = (int)(0xFFFFFFFFu - (uint32_t)wm);
-    float pw = 0.0f;
-#pragma unroll
-    for (int i = 0; i < P; i++) {  // selects, not a computed index: key[] stays in registers
-      const bool hit = key[i] == wm;
-      pw = hit ? pv[i] : pw;
-      key[i] = hit ? 0ull : key[i];
+    __syncthreads();
+    // 4. rank of each kept candidate among the kept candidates: NS threads
+    //    per candidate slot, each over a share of the slots, summed by shuffles
+    const int ns_log = __builtin_ctz(NS), c = tid >> ns_log, part = tid & (NS - 1);
+    const int chunk = (NC + NS - 1) >> ns_log;
+    int r = 0;
+    uint64_t k0 = 0ull;
+    if (c < NC) {
+      k0 = l_cand[c];
+      if (k0) {
+        const int j0 = part * chunk, j1 = min(NC, j0 + chunk);
+#pragma unroll 8
+        for (int j = j0; j < j1; j++) r += l_cand[j] > k0;
+      }
     }
-    pw = __builtin_bit_cast(float, readlane_u32(__builtin_bit_cast(uint32_t, pw), e / P));
-    if (lane == r) { my_sel = e; my_p = pw; }
+    for (int o = 1; o < NS; o <<= 1) r += __shfl_xor(r, o, 64);
+    if (c < NC && part == 0 && k0 && r < K) {
+      const int e = (int)(0xFFFFFFFFu - (uint32_t)k0);
+      l_sel[r] = e;
+      l_sp[r] = l_p[e];
+    }
+    __syncthreads();
+  } else if (G > 1) {
+    // 3. the topk_group best groups by (best + second-best score, group index)
+    auto gkey = [&](int g) -> uint64_t {
+      const float gs = gsz >= 2 ? l_gb[2 * g] + l_gb[2 * g + 1] : l_gb[2 * g];
+      return gs > -__builtin_inff() ? (((uint64_t)ord_f32(gs) << 32) | (0xFFFFFFFFu - (uint32_t)g)) : 0ull;
+    };
+    if (tid < G) {
+      const uint64_t mine = gkey(tid);
+      int r = 0;
+      for (int g2 = 0; g2 < G; g2++) r += gkey(g2) > mine;
+      l_keep[tid] = mine && r < a.topk_group;
+    }
+    __syncthreads();
+    // 4. rank of each kept candidate among all kept candidates: the slot
+    for (int i = tid; i < G * Kc; i += 256) {
+      const uint64_t k0 = l_cand[i];
+      if (!k0 || !l_keep[i / Kc]) continue;
+      int r = 0;
+      for (int g2 = 0; g2 < G; g2++) {
+        if (!l_keep[g2]) continue;
+        for (int j = 0; j < Kc; j++) r += l_cand[g2 * Kc + j] > k0;
+      }
+      if (r < K) {
+        const int e = (int)(0xFFFFFFFFu - (uint32_t)k0);
+        l_sel[r] = e;
+        l_sp[r] = l_p[e];
+      }
+    }
+    __syncthreads();
   }
-  float sum = 0.0f;
-  for (int j = 0; j < K; j++) {
-    const int sj = (int)readlane_u32((uint32_t)my_sel, j);
-    const float pj = __builtin_bit_cast(float, readlane_u32(__builtin_bit_cast(uint32_t, my_p), j));
-    sum += sj >= 0 ? pj : 0.0f;
-  }
-  if (sum < 6.103515625e-5f) sum = 6.103515625e-5f;
-  if (lane < K) {
-    const float wgt = (my_sel >= 0 ? my_p : 0.0f) / (sum / a.route_scale);
+  // 5. weights: probabilities over their slot-ordered sum, times route_scale
+  if (tid < K) {
+    float sum = 0.0f;  // empty slots hold +0
+#pragma unroll 8
+    for (int j = 0; j < K; j++) sum += l_sp[j];
+    if (sum < 6.103515625e-5f) sum = 6.103515625e-5f;
+    const int e = l_sel[tid];
+    const float wgt = (e >= 0 ? l_sp[tid] : 0.0f) / (sum / a.route_scale);
     if (global) {
-      stc<kCoh>(a.selected + (size_t)t * K + lane, my_sel);
-      stc<kCoh>(a.weights + (size_t)t * K + lane, wgt);
+      stc<kCoh>(a.selected + (size_t)t * K + tid, e);
+      stc<kCoh>(a.weights + (size_t)t * K + tid, wgt);
     }
-    if (s_sel) { s_sel[lane] = my_sel; s_w[lane] = wgt; }
+    if (s_sel) { s_sel[tid] = e; s_w[tid] = wgt; }
   }
-}
-
-template <bool kCoh, int P>
-__device__ __forceinline__ bool select_wave_fits(const RouterSelectArgs& a) {
-  if (a.E != 64 * P) return false;
-  const int G = a.n_group > 1 ? a.n_group : 1;
-  if (G == 1) return true;
-  const int gsz = a.E / G;
-  if (gsz % P) return false;
-  const int lpg = gsz / P;
-  return lpg == 1 || lpg == 2 || lpg == 4 || lpg == 8 || lpg == 16;
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------------------
@@ -868,16 +853,29 @@ __device__ __forceinline__ float iq2_blk_dot(const uint32_t* w, uint32_t sel, ui
   int32_t bsum = 0;
 #pragma unroll
   for (int ib = 0; ib < 8; ib++) {
-    const uint32_t aux0 = __builtin_amdgcn_perm(w[2 * ib + 1], w[2 * ib], sel);
-    const uint32_t aux1 = __builtin_amdgcn_perm(w[2 * ib + 2], w[2 * ib + 1], sel);
-    const uint4 qa = *(const uint4*)(q8 + ib * 32);
-    const uint4 qb = *(const uint4*)(q8 + ib * 32 + 16);
+    // opaque zero depending on the running sum (as in iq2_block_dot): the
+    // sub-block's lookups stay after the previous one's arithmetic, which
+    // holds the kernel to ~116 VGPRs (4 waves per SIMD) instead of 254
+    int z = 0;
+    asm volatile("" : "+v"(z) : "v"(bsum));
+    const uint32_t aux0 = __builtin_amdgcn_perm(w[2 * ib + 1], w[2 * ib], sel) + z;
+    const uint32_t aux1 = __builtin_amdgcn_perm(w[2 * ib + 2], w[2 * ib + 1], sel) + z;
+    const uint4 qa = *(const uint4*)(q8 + ib * 32 + z);
+    const uint4 qb = *(const uint4*)(q8 + ib * 32 + 16 + z);
     int32_t pos = 0, neg = 0;
     const uint32_t qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
     for (int g = 0; g < 4; g++) {
+#if defined(DSM_X_NOGRID)
+      const uint64_t gv = ((uint64_t)(aux0 >> g) << 32) | (aux0 >> (8 * g));
+#else
       const uint64_t gv = t->grid[(aux0 >> (8 * g)) & 0xFF];
+#endif
+#if defined(DSM_X_NOMASK)
+      const uint64_t mv = ((uint64_t)(aux1 << g) << 32) | (aux1 >> (7 * g));
+#else
       const uint64_t mv = t->mask[(aux1 >> (7 * g)) & 127];
+#endif
       pos = dot4((uint32_t)gv, qv[2 * g], pos);
       pos = dot4((uint32_t)(gv >> 32), qv[2 * g + 1], pos);
       neg = dot4((uint32_t)(gv & mv), qv[2 * g], neg);
@@ -905,16 +903,16 @@ __shared__ Iq2Tables g_tab_rows;
 
 // kNit = blocks per lane, ceil(nb / 4): a compile-time count keeps every load
 // unconditional and the wait counts exact.
-// With `rs` (fuse_sel = P) wave 0 of the workgroup runs the token's routing
-// (moe.rs:177-287) itself, into LDS, while the activation words are in
-// flight; the workgroup of tile 0 of the token's first pair also stores it
-// to rs->selected / rs->weights for the down launch.
+// With `rs` (fuse_sel) the workgroup runs the token's routing (moe.rs:177-287)
+// itself, into LDS, while the activation words are in flight; the workgroup
+// of tile 0 of the token's first pair also stores it to rs->selected /
+// rs->weights for the down launch.
 __shared__ int32_t g_sel_rows[32];
 __shared__ float g_wgt_rows[32];
 
 template <int kNit>
 __device__ __forceinline__ void role_gate_up_rows(const GateUpArgs& a, int tile, int pair, uint8_t* smem,
-                                                  const RouterSelectArgs* rs = nullptr, int rsP = 0) {
+                                                  const RouterSelectArgs* rs = nullptr) {
   const int nb = a.d >> 8, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
   GuLds l = gu_lds(a, smem);
   l.tab = &g_tab_rows;  // static LDS: the table addresses fold into the lookups
@@ -936,13 +934,9 @@ __device__ __forceinline__ void role_gate_up_rows(const GateUpArgs& a, int tile,
   int e;
   float wgt;
   if (rs) {
-    if (wv == 0) {
-      const bool g = tile == 0 && pair % a.k == 0;
-      if (rsP == 4) select_wave<false, 4>(*rs, tok, g_sel_rows, g_wgt_rows, g);
-      else if (rsP == 2) select_wave<false, 2>(*rs, tok, g_sel_rows, g_wgt_rows, g);
-      else select_wave<false, 1>(*rs, tok, g_sel_rows, g_wgt_rows, g);
-    }
-    __syncthreads();
+    // LDS scratch of the selection: the dynamic area, written by the staging
+    // only after the selection's last barrier
+    role_select<false>(*rs, tok, smem, g_sel_rows, g_wgt_rows, tile == 0 && pair % a.k == 0);
     e = g_sel_rows[pair % a.k];
     wgt = g_wgt_rows[pair % a.k];
   } else {
@@ -1752,95 +1746,6 @@ __device__ __forceinline__ void dn_unit(const DownArgs& a, int tile, int tok, ui
 }
 
 
-template <bool kCoh>
-__device__ __forceinline__ void role_select(const RouterSelectArgs& a, int t, uint8_t* smem) {
-  const int E = a.E;
-  uint64_t* s_key = (uint64_t*)smem;
-  uint64_t* s_gkey = s_key + E;
-  float* s_p = (float*)(s_gkey + 64);
-  float* s_sc = s_p + E;
-  float* s_b1 = s_sc + E;
-  float* s_b2 = s_b1 + 64;
-  int* s_keep = (int*)(s_b2 + 64);
-  int* s_sel = s_keep + 64;
-  const int tid = threadIdx.x;
-  {
-    // E = 64, 128, 256 (one instantiation inside the decode launch: E = 256)
-    int fast = 0;
-    if (!kCoh && select_wave_fits<kCoh, 1>(a)) fast = 1;
-    else if (!kCoh && select_wave_fits<kCoh, 2>(a)) fast = 2;
-    else if (select_wave_fits<kCoh, 4>(a)) fast = 4;
-    if (fast) {
-      if (tid < 64) {
-        if (!kCoh && fast == 1) select_wave<kCoh, 1>(a, t);
-        else if (!kCoh && fast == 2) select_wave<kCoh, 2>(a, t);
-        else select_wave<kCoh, 4>(a, t);
-      }
-      __syncthreads();
-      return;
-    }
-  }
-  const int K = a.k, G = a.n_group > 1 ? a.n_group : 1, gsz = E / G;
-  for (int e = tid; e < E; e += 256) {
-    const float pv = __builtin_sqrtf(softplus_dsm(ldc<kCoh>(a.logits + (size_t)t * E + e)));
-    const float sc = a.has_bias ? pv + a.bias[e] : pv;
-    s_p[e] = pv;
-    s_sc[e] = sc;
-    s_key[e] = sc > -__builtin_inff() ? (((uint64_t)ord_f32(sc) << 32) | (0xFFFFFFFFu - (uint32_t)e)) : 0ull;
-    if (a.probs) a.probs[(size_t)t * E + e] = pv;
-  }
-  if (tid < 64) { s_b1[tid] = -__builtin_inff(); s_b2[tid] = -__builtin_inff(); s_keep[tid] = G == 1; }
-  if (tid < 32) s_sel[tid] = -1;
-  __syncthreads();
-  if (G > 1) {
-    for (int e = tid; e < E; e += 256) {
-      const uint64_t k0 = s_key[e];
-      if (!k0) continue;
-      const int g = e / gsz;
-      int r = 0;
-#pragma unroll 8
-      for (int e2 = g * gsz; e2 < (g + 1) * gsz; e2++) r += s_key[e2] > k0;
-      if (r == 0) s_b1[g] = s_sc[e];
-      if (r == 1) s_b2[g] = s_sc[e];
-    }
-    __syncthreads();
-    if (tid < G) {
-      const float gs = gsz >= 2 ? s_b1[tid] + s_b2[tid] : s_b1[tid];
-      s_gkey[tid] = gs > -__builtin_inff() ? (((uint64_t)ord_f32(gs) << 32) | (0xFFFFFFFFu - (uint32_t)tid)) : 0ull;
-    }
-    __syncthreads();
-    if (tid < G && s_gkey[tid]) {
-      int r = 0;
-      for (int g2 = 0; g2 < G; g2++) r += s_gkey[g2] > s_gkey[tid];
-      s_keep[tid] = r < a.topk_group;
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += 256)
-      if (!s_keep[e / gsz]) s_key[e] = 0ull;
-    __syncthreads();
-  }
-  for (int e = tid; e < E; e += 256) {
-    const uint64_t k0 = s_key[e];
-    if (!k0) continue;
-    int r = 0;
-#pragma unroll 16
-    for (int e2 = 0; e2 < E; e2++) r += s_key[e2] > k0;
-    if (r < K) s_sel[r] = e;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float sum = 0.0f;
-    for (int j = 0; j < K; j++) sum += s_sel[j] >= 0 ? s_p[s_sel[j]] : 0.0f;
-    if (sum < 6.103515625e-5f) sum = 6.103515625e-5f;
-    for (int j = 0; j < K; j++) {
-      const int e = s_sel[j];
-      stc<kCoh>(a.selected + (size_t)t * K + j, e);
-      stc<kCoh>(a.weights + (size_t)t * K + j, (e >= 0 ? s_p[e] : 0.0f) / (sum / a.route_scale));
-    }
-  }
-  __syncthreads();
-}
-
 }  // namespace
 
 // ===========================================================================
@@ -1850,6 +1755,17 @@ __device__ __forceinline__ void role_select(const RouterSelectArgs& a, int t, ui
 // Router logits + Q8_K(x) + Q8_0(x) (blockDim 256): one router row, four
 // Q8_K blocks or 32 Q8_0 blocks (8 when in_dim is not a multiple of 32) per
 // workgroup.
+// All threads: make this workgroup's coherent stores complete, then run `f`
+// on thread 0 and broadcast its bool result.
+template <class F>
+__device__ __forceinline__ bool stores_done_then(int* s_flag, F f) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) *s_flag = f() ? 1 : 0;
+  __syncthreads();
+  return *s_flag != 0;
+}
+
 extern "C" __global__ __launch_bounds__(256) void dsmoe_prep(const PrepArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   int w = blockIdx.x;
@@ -1886,26 +1802,15 @@ extern "C" __global__ __launch_bounds__(1024) void dsmoe_up(const UpArgs a) {
 __device__ __forceinline__ void role_gate_up_rows_any(const UpArgs& a, int tile, int pair, uint8_t* smem) {
   const RouterSelectArgs* rs = a.fuse_sel ? &a.sel : nullptr;
   switch ((a.gu.d + 1023) >> 10) {  // blocks per lane (d <= 8192)
-    case 1: role_gate_up_rows<1>(a.gu, tile, pair, smem, rs, a.fuse_sel); break;
-    case 2: role_gate_up_rows<2>(a.gu, tile, pair, smem, rs, a.fuse_sel); break;
-    case 3: role_gate_up_rows<3>(a.gu, tile, pair, smem, rs, a.fuse_sel); break;
-    case 4: role_gate_up_rows<4>(a.gu, tile, pair, smem, rs, a.fuse_sel); break;
-    case 5: role_gate_up_rows<5>(a.gu, tile, pair, smem, rs, a.fuse_sel); break;
-    case 6: role_gate_up_rows<6>(a.gu, tile, pair, smem, rs, a.fuse_sel); break;
-    case 7: role_gate_up_rows<7>(a.gu, tile, pair, smem, rs, a.fuse_sel); break;
-    default: role_gate_up_rows<8>(a.gu, tile, pair, smem, rs, a.fuse_sel); break;
+    case 1: role_gate_up_rows<1>(a.gu, tile, pair, smem, rs); break;
+    case 2: role_gate_up_rows<2>(a.gu, tile, pair, smem, rs); break;
+    case 3: role_gate_up_rows<3>(a.gu, tile, pair, smem, rs); break;
+    case 4: role_gate_up_rows<4>(a.gu, tile, pair, smem, rs); break;
+    case 5: role_gate_up_rows<5>(a.gu, tile, pair, smem, rs); break;
+    case 6: role_gate_up_rows<6>(a.gu, tile, pair, smem, rs); break;
+    case 7: role_gate_up_rows<7>(a.gu, tile, pair, smem, rs); break;
+    default: role_gate_up_rows<8>(a.gu, tile, pair, smem, rs); break;
   }
-}
-
-// All threads: make this workgroup's coherent stores complete, then run `f`
-// on thread 0 and broadcast its bool result.
-template <class F>
-__device__ __forceinline__ bool stores_done_then(int* s_flag, F f) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) *s_flag = f() ? 1 : 0;
-  __syncthreads();
-  return *s_flag != 0;
 }
 
 // With fuse_midq the quantization of the mid rows happens here too: each
