@@ -866,16 +866,8 @@ __device__ __forceinline__ float iq2_blk_dot(const uint32_t* w, uint32_t sel, ui
     const uint32_t qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
     for (int g = 0; g < 4; g++) {
-#if defined(DSM_X_NOGRID)
-      const uint64_t gv = ((uint64_t)(aux0 >> g) << 32) | (aux0 >> (8 * g));
-#else
       const uint64_t gv = t->grid[(aux0 >> (8 * g)) & 0xFF];
-#endif
-#if defined(DSM_X_NOMASK)
-      const uint64_t mv = ((uint64_t)(aux1 << g) << 32) | (aux1 >> (7 * g));
-#else
       const uint64_t mv = t->mask[(aux1 >> (7 * g)) & 127];
-#endif
       pos = dot4((uint32_t)gv, qv[2 * g], pos);
       pos = dot4((uint32_t)(gv >> 32), qv[2 * g + 1], pos);
       neg = dot4((uint32_t)(gv & mv), qv[2 * g], neg);
