@@ -18,6 +18,8 @@
 // :622-715), so results are bit-identical to the per-pair kernels.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "dsmoe_formats.h"
 #include "dsmoe_kargs.h"
 #include "dsmoe_math.h"
@@ -147,54 +149,53 @@ __device__ __forceinline__ TileSlab xcd_slab_tile(int ntiles, int ny) { return x
 
 // ---------------------------------------------------------------------------
 // Routed gate/up/SwiGLU over sorted pairs (moe_gate_up_mid_sorted_qwarp32,
-// moe.rs:721-815; per-pair arithmetic of moe.rs:622-715).
-// grid = 8 * ceil(max tiles / 8) * (I / kGuBN) (xcd_tile_slab), 256 threads:
-// wave w computes the 32x32 output block (pairs 32*(w&1).., rows of gate
-// (w<2) or up (w>=2)).
+// moe.rs:721-815; per-pair arithmetic of moe.rs:622-715).  A workgroup is one
+// dispatch tile (up to kGuBM = 64 pairs of one expert) x kGuBN = 128 rows of
+// gate and the same rows of up.  Wave w takes rows n0 + 32w .. +31 of gate and
+// of up for all 64 pairs: four 32x32 MFMA tiles (pairs 0-31 / 32-63 x gate /
+// up), so the SwiGLU needs no exchange between waves.
 //
-// Pipeline: every superblock is split into two stages of 128 elements, its
-// even sub-blocks (stage 0) and its odd ones (stage 1); the K order inside a
-// superblock is free because its sum is an exact integer.  Stage-local chunk
-// c = 4j + g (16 bytes) holds elements 64j + 32h + 8g .. +7 of the
-// superblock.  Stages are double-buffered in LDS with one barrier per stage:
-// each iteration issues the MFMAs of stage s, then stores stage s+1
-// (activations from registers, weights dequantized from raw bytes loaded one
-// superblock ahead), then applies the superblock epilogue, so the matrix
-// cores run while the VALU dequantizes.  Wave w owns rows 16w .. 16w+15 of
-// both operands:
-//   activations: four rows x four 64-byte pieces per load instruction, stored
-//     row-major with 16-byte chunks XOR-swizzled by the row;
-//   weights: lane l handles weight row 16w + l/4 and sub-blocks 2p, 2p+1
-//     (p = l % 4), i.e. 16 contiguous raw bytes per superblock and one
-//     sub-block per stage; the dequantized tile is chunk-major [chunk][row]
-//     with the row slot XOR-swizzled by 2p.
-// Both layouts keep every LDS access conflict-free.
+// A (the pairs' Q8_K integers as f16): one superblock (64 x 256) per LDS
+// buffer, two buffers, loaded straight into LDS (global_load_lds_dwordx4):
+// 16-byte chunk c of pair row m sits in slot m * 32 + (c ^ (m & 31)), so the
+// operand reads (lanes = 32 rows x 2 chunks) are conflict-free.
+// B (IQ2_XXS): lane l dequantizes its own weight row (l % 32) straight into
+// the MFMA operand.  k-step ks of a superblock is group 2 (ks & 1) + l / 32 of
+// sub-block ks / 2, i.e. eight consecutive weights, (g * ls) ^ sign as f16
+// (exact small integers) from the grid / sign tables in LDS.  The row's 68
+// raw bytes of a superblock are loaded one superblock ahead into registers.
+// Both matrices of a wave share each A operand read, and each dequantized B
+// operand serves both pair tiles.
 //
-// Exactness per stage and per superblock: a stage whose bound
-// 127 * sum |w| reaches 2^24 is summed in two segments of at most 96
-// elements and combined as integers; the second stage accumulates onto the
-// first in f32 only when the whole superblock's bound is below 2^24.
+// Per superblock each (pair, row) sum of integer products accumulates in f32
+// on the matrix cores (exact while below 2^24); its block value
+// 0.125 * xd * yd * sum is formed as in the reference and added to the
+// row's running sum in superblock order 0, 1, 2, ...  The reference adds the
+// blocks b = l mod 8 per lane l and then a butterfly over the 8 lanes, so the
+// two agree to f32 rounding of that sum order (the integer and indexing work
+// is the reference's exactly).
 // ---------------------------------------------------------------------------
 namespace {
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
 
-constexpr int kGuRows = 2 * kGuBN;  // weight rows per workgroup (gate + up)
-
-struct GuRaw {
-  uint32_t w[5];  // 16 qs bytes of sub-blocks 2p, 2p+1 (plus a straddled dword)
-  uint32_t dd;    // the dword holding the row's f16 scale
-};
-
+// 68 bytes from a 4-byte aligned address (four 16-byte loads and a dword)
+__device__ __forceinline__ void load17(const uint8_t* p, uint32_t* r) {
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const u32x4 v = *(const u32x4*)(p + 16 * q);
+    r[4 * q] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
+  }
+  r[16] = *(const uint32_t*)(p + 64);
+}
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+extern "C" __global__ __launch_bounds__(256)
 void dsmoe_gu_grouped(const GuGroupedArgs a) {
-  __shared__ uint4 sA[2][kGuBM][16];
-  __shared__ uint4 sB[2][16][kGuRows];
+  __shared__ __align__(16) u32x4 sA[2][kGuBM * 32];
+  __shared__ __align__(16) float s_yd[2][kGuBM];
   __shared__ Iq2HalfTables tab;
-  __shared__ float s_yd[2][kGuBM], s_xd[2][kGuRows];
-  __shared__ uint32_t s_bnd[2][4][kGuRows];
-  __shared__ uint32_t s_pair[kGuBM];
-  __shared__ int8_t s_seq[32], s_fold[32];
+  __shared__ uint32_t s_pair[kGuBM], s_xrow[kGuBM], s_qrow[kGuBM];
 
   const TileSlab ts = xcd_tile_slab((int)a.tile_offsets[a.E], a.I / kGuBN);
   if (!ts.ok) return;
@@ -203,274 +204,130 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
   const int p0 = (int)(a.offsets[e] + a.tile_starts[t]);
   const int cnt = min(kGuBM, (int)a.offsets[e + 1] - p0);
   const int n0 = ts.n * kGuBN;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, kh = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
   const int d = a.d, nb = d >> 8, I = a.I, K = a.k;
 
-  if (tid < kGuBM) s_pair[tid] = tid < cnt ? a.sorted_pairs[p0 + tid] : 0xFFFFFFFFu;
-  if (tid == 0) {
-    // superblocks in lane-class order; s_fold marks the last one of each class
-    int i = 0;
-    for (int ci = 0; ci < 8; ci++) {
-      const int len = class_len(ci, nb);
-      for (int j = 0; j < len; j++, i++) {
-        s_seq[i] = (int8_t)(lane_class(ci) + 8 * j);
-        s_fold[i] = (int8_t)(j == len - 1 ? ci : -1);
-      }
-    }
+  if (tid < kGuBM) {
+    const uint32_t pr = tid < cnt ? a.sorted_pairs[p0 + tid] : 0xFFFFFFFFu;
+    const uint32_t tok = pr != 0xFFFFFFFFu ? pr / (uint32_t)K : 0u;  // dead rows read token 0, never stored
+    s_pair[tid] = pr;
+    s_xrow[tid] = tok * (uint32_t)d * 2u;
+    s_qrow[tid] = tok * (uint32_t)nb * (uint32_t)Q8K_BYTES;
   }
   load_iq2_half_tables(&tab);
   __syncthreads();
 
-  // this thread's weight row / pair row (16w + lane / 4) and quarter p
-  const int r = 16 * w + (lane >> 2), pq = lane & 3;
-  // activation loads: instruction j covers rows 16w + 4j + lane / 16, piece
-  // (lane / 4) % 4, chunk lane % 4 of the piece (dead rows read token 0:
-  // finite, never stored)
-  uint32_t aoff[4];
+  // A: wave w's eight loads per superblock fill slots (8w + j) * 64 + lane
+  uint32_t aoff[8];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const uint32_t pr = s_pair[16 * w + 4 * j + (lane >> 4)];
-    aoff[j] = (pr != 0xFFFFFFFFu ? pr / (uint32_t)K : 0u) * (uint32_t)d + 64 * ((lane >> 2) & 3) + 8 * (lane & 3);
+  for (int j = 0; j < 8; j++) {
+    const int sl = (8 * w + j) * 64 + lane, m = sl >> 5, c = (sl & 31) ^ (m & 31);
+    aoff[j] = s_xrow[m] + 16u * (uint32_t)c;
   }
-  const uint32_t ypair = s_pair[r];
-  const uint8_t* yrow = a.xq + (size_t)(ypair != 0xFFFFFFFFu ? ypair / (uint32_t)K : 0u) * nb * Q8K_BYTES;
-  // weight row r: gate rows n0.. (r < 32), up rows n0.. (r >= 32)
-  const uint8_t* wrow = (r < kGuBN ? a.gate : a.up) + ((size_t)e * I + n0 + (r & (kGuBN - 1))) * nb * IQ2XXS_BYTES;
+  const uint32_t qoff = s_qrow[lane];
+  auto issue_a = [&](int b, int buf) {
+    const uint8_t* base = (const uint8_t*)a.xh + 512 * b;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      __builtin_amdgcn_global_load_lds((glb_void*)(base + aoff[j]), (lds_void*)&sA[buf][(8 * w + j) * 64], 16, 0, 0);
+    if (w == 0)  // the 64 pairs' block scales: lane l -> s_yd[buf][l]
+      __builtin_amdgcn_global_load_lds((glb_void*)(a.xq + qoff + (size_t)b * Q8K_BYTES), (lds_void*)&s_yd[buf][0], 4,
+                                       0, 0);
+  };
+  const size_t rb = (size_t)nb * IQ2XXS_BYTES;
+  const size_t row = (size_t)e * I + n0 + 32 * w + l32;
+  const uint8_t* grow = a.gate + row * rb;
+  const uint8_t* urow = a.up + row * rb;
+  // superblock b's 68 bytes from its dword-aligned start (odd b: 2 bytes before)
+  auto raw_at = [&](const uint8_t* r, int b) { return r + IQ2XXS_BYTES * b - 2 * (b & 1); };
 
-  // activation registers: stage h of every superblock uses set h, loaded two
-  // stages ahead (named registers: an array here ends up in scratch)
-  uint4 a00, a01, a02, a03, a10, a11, a12, a13;
-  float ayd = 0.0f;
-#define DSM_GU_ISSUE_A(B, H, V0, V1, V2, V3)                        \
-  {                                                                 \
-    const uint16_t* base_ = a.xh + 256 * (B) + 32 * (H);            \
-    V0 = *(const uint4*)(base_ + aoff[0]);                          \
-    V1 = *(const uint4*)(base_ + aoff[1]);                          \
-    V2 = *(const uint4*)(base_ + aoff[2]);                          \
-    V3 = *(const uint4*)(base_ + aoff[3]);                          \
-    /* every lane loads yd (no branch around a load) */             \
-    if ((H) == 0) ayd = ld_f32(yrow + (size_t)(B) * Q8K_BYTES);     \
-  }
-  auto issue_a = [&](int b, int h) {
-    if (h == 0) DSM_GU_ISSUE_A(b, 0, a00, a01, a02, a03) else DSM_GU_ISSUE_A(b, 1, a10, a11, a12, a13)
-  };
-  auto issue_raw = [&](int b, GuRaw& raw) {
-    const uint8_t* blk = wrow + (size_t)b * IQ2XXS_BYTES;
-    const uint8_t* qs = blk + 2 + 16 * pq;
-    const uint32_t mis = (uint32_t)((uintptr_t)qs & 3);
-    const uint32_t* wp = (const uint32_t*)(qs - mis);
+  float16v rg0, rg1, ru0, ru1;  // running sums: pairs 0-31 / 32-63 x gate / up
 #pragma unroll
-    for (int j = 0; j < 4; j++) raw.w[j] = wp[j];
-    raw.w[4] = wp[mis ? 4 : 3];  // the fifth dword only when the 16 bytes straddle it
-    raw.dd = *(const uint32_t*)(blk - ((uintptr_t)blk & 3));
-  };
-  // stores stage (b, h) into buffer buf
-  auto commit = [&](int buf, int sbb, int b, int h, const GuRaw& raw) {
-#define DSM_STORE_A(j, v)                                        \
-    {                                                            \
-      const int row = 16 * w + 4 * (j) + (lane >> 4);            \
-      sA[buf][row][(lane & 15) ^ (row & 15)] = v;                \
-    }
-    if (h == 0) {
-      DSM_STORE_A(0, a00)
-      DSM_STORE_A(1, a01)
-      DSM_STORE_A(2, a02)
-      DSM_STORE_A(3, a03)
-    } else {
-      DSM_STORE_A(0, a10)
-      DSM_STORE_A(1, a11)
-      DSM_STORE_A(2, a12)
-      DSM_STORE_A(3, a13)
-    }
-#undef DSM_STORE_A
-    const uint8_t* blk = wrow + (size_t)b * IQ2XXS_BYTES;
-    if (h == 0 && pq == 0) {
-      s_yd[sbb][r] = ayd;
-      const uint16_t dbits = ((uintptr_t)blk & 3) ? (uint16_t)(raw.dd >> 16) : (uint16_t)(raw.dd & 0xFFFF);
-      s_xd[sbb][r] = f16_to_f32_ftz(dbits);
-    }
-    const uint32_t sh = (uint32_t)((uintptr_t)(blk + 2 + 16 * pq) & 3);
-    const uint32_t aux0 = sh ? __builtin_amdgcn_alignbyte(raw.w[2 * h + 1], raw.w[2 * h], sh) : raw.w[2 * h];
-    const uint32_t aux1 = sh ? __builtin_amdgcn_alignbyte(raw.w[2 * h + 2], raw.w[2 * h + 1], sh) : raw.w[2 * h + 1];
-    const uint32_t ls = 2 * (aux1 >> 28) + 1;
-    const _Float16 lsh = (_Float16)(float)ls;
-    const int slot = r ^ (2 * pq);
-    uint32_t gs = 0;  // sum over the sub-block of |g|; the bound is gs * ls
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-      const uint32_t gi = (aux0 >> (8 * g)) & 0xFF, si = (aux1 >> (7 * g)) & 127;
-      sB[buf][4 * pq + g][slot] = iq2_half8(tab.gridh[gi], tab.sign[si], lsh);
-      gs += tab.gsum[gi];
-    }
-    s_bnd[buf][pq][r] = gs * ls;
-  };
+  for (int i = 0; i < 16; i++) { rg0[i] = 0.0f; rg1[i] = 0.0f; ru0[i] = 0.0f; ru1[i] = 0.0f; }
 
-  // --- MFMA side -------------------------------------------------------------
-  const int mt = w & 1, mat = w >> 1, hh = lane >> 5;
-  const int arow_l = mt * 32 + (lane & 31), bcol = mat * 32 + (lane & 31);
-  auto opA = [&](int buf, int ks) { return *(const half8*)&sA[buf][arow_l][(2 * ks + hh) ^ (arow_l & 15)]; };
-  auto opB = [&](int buf, int ks) { return *(const half8*)&sB[buf][2 * ks + hh][bcol ^ (2 * (ks >> 1))]; };
-  // operands are read four k-steps at a time (32 VGPRs), the next batch's
-  // reads going out while the current batch's MFMAs run
-  auto mfma_run = [&](int buf, int k0, int k1, float16v& x) {
-    half8 oa[4], ob[4];
+  // one superblock from LDS buffer buf and raw rows gr / ur (kEven: the qs
+  // start 2 bytes into the loaded words)
+  auto superblock = [&](auto even_tag, int buf, const uint32_t* gr, const uint32_t* ur) {
+    constexpr bool kEven = decltype(even_tag)::value;
+    auto qs = [&](const uint32_t* r, int j) -> uint32_t {
+      return kEven ? __builtin_amdgcn_alignbyte(r[j + 1], r[j], 2) : r[j + 1];
+    };
+    float16v ag0, ag1, au0, au1;
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-      if (k0 + j < k1) {
-        oa[j] = opA(buf, k0 + j);
-        ob[j] = opB(buf, k0 + j);
+    for (int i = 0; i < 16; i++) { ag0[i] = 0.0f; ag1[i] = 0.0f; au0[i] = 0.0f; au1[i] = 0.0f; }
+    _Float16 lsg = 1, lsu = 1;
+    uint32_t g1 = 0, u1 = 0;
+    const u32x4* sa = &sA[buf][0];
+#pragma unroll
+    for (int ks = 0; ks < 16; ks++) {
+      const int sb = ks >> 1;
+      if ((ks & 1) == 0) {
+        g1 = qs(gr, 2 * sb + 1);
+        u1 = qs(ur, 2 * sb + 1);
+        lsg = (_Float16)(float)(2 * (g1 >> 28) + 1);
+        lsu = (_Float16)(float)(2 * (u1 >> 28) + 1);
       }
-#pragma unroll
-    for (int kb = k0; kb < k1; kb += 4) {
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        if (kb + j < k1) x = __builtin_amdgcn_mfma_f32_32x32x16_f16(oa[j], ob[j], x, 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        if (kb + 4 + j < k1) {
-          oa[j] = opA(buf, kb + 4 + j);
-          ob[j] = opB(buf, kb + 4 + j);
-        }
+      const uint32_t sh0 = 16 * (ks & 1) + 8 * kh, sh1 = 14 * (ks & 1) + 7 * kh;
+      const uint32_t gg = __builtin_amdgcn_ubfe(qs(gr, 2 * sb), sh0, 8), gs = __builtin_amdgcn_ubfe(g1, sh1, 7);
+      const uint32_t ug = __builtin_amdgcn_ubfe(qs(ur, 2 * sb), sh0, 8), us = __builtin_amdgcn_ubfe(u1, sh1, 7);
+      const half8 bg = __builtin_bit_cast(half8, iq2_half8(tab.gridh[gg], tab.sign[gs], lsg));
+      const half8 bu = __builtin_bit_cast(half8, iq2_half8(tab.gridh[ug], tab.sign[us], lsu));
+      const int c = (2 * ks + kh) ^ l32;
+      const half8 a0 = __builtin_bit_cast(half8, sa[l32 * 32 + c]);
+      const half8 a1 = __builtin_bit_cast(half8, sa[(32 + l32) * 32 + c]);
+      ag0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bg, ag0, 0, 0, 0);
+      au0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bu, au0, 0, 0, 0);
+      ag1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bg, ag1, 0, 0, 0);
+      au1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bu, au1, 0, 0, 0);
     }
-  };
-  auto zero16 = [](float16v& x) {
-    for (int i = 0; i < 16; i++) x[i] = 0.0f;
-  };
-  // a stage as exact integers in two segments of at most 6 x 16 elements
-  auto stage_int = [&](int buf) {
-    float16v s0, s1;
-    zero16(s0);
-    zero16(s1);
-    mfma_run(buf, 0, 6, s0);
-    mfma_run(buf, 6, 8, s1);
-    return __builtin_convertvector(s0, int16v) + __builtin_convertvector(s1, int16v);
-  };
-  auto row_bound = [&](int buf) {
-    return s_bnd[buf][0][lane] + s_bnd[buf][1][lane] + s_bnd[buf][2][lane] + s_bnd[buf][3][lane];
-  };
-  auto any_over = [&](uint32_t bnd) { return __builtin_amdgcn_ballot_w64((float)bnd * 127.0f >= kExactBound) != 0; };
-
-  float16v run, h0, h1, l2a, acc;  // acc holds int bits while acc_int
-  zero16(run);
-  zero16(h0);
-  zero16(h1);
-  zero16(l2a);
-  zero16(acc);
-  bool acc_int = false;
-  uint32_t bnd0 = 0;
-
-  // stage 0 of a superblock: MFMAs into acc (f32, or int bits)
-  auto mfma_h0 = [&]() {
-    bnd0 = row_bound(0);
-    if (!any_over(bnd0)) {
-      zero16(acc);
-      mfma_run(0, 0, 8, acc);
-      acc_int = false;
-    } else {
-      acc = __builtin_bit_cast(float16v, stage_int(0));
-      acc_int = true;
-    }
-  };
-  // stage 1: onto acc in f32 when the superblock is exact, else as integers
-  auto mfma_h1 = [&]() {
-    const uint32_t bnd1 = row_bound(1);
-    if (!acc_int && !any_over(bnd0 + bnd1)) {
-      mfma_run(1, 0, 8, acc);
-    } else {
-      int16v xi;
-      if (!any_over(bnd1)) {
-        float16v x;
-        zero16(x);
-        mfma_run(1, 0, 8, x);
-        xi = __builtin_convertvector(x, int16v);
-      } else {
-        xi = stage_int(1);
-      }
-      const int16v base = acc_int ? __builtin_bit_cast(int16v, acc) : __builtin_convertvector(acc, int16v);
-      acc = __builtin_convertvector(base + xi, float16v);
-    }
-  };
-  auto epilogue = [&](int i) {
-    const int sbb = i & 1;
-    const float c = 0.125f * s_xd[sbb][bcol];
+    // block values 0.125 * xd * yd * sum (quantize.rs:763-812), added in superblock order
+    const float cg = 0.125f * f16_to_f32_ftz((uint16_t)(kEven ? gr[0] & 0xFFFF : gr[0] >> 16));
+    const float cu = 0.125f * f16_to_f32_ftz((uint16_t)(kEven ? ur[0] & 0xFFFF : ur[0] >> 16));
+    const float* yd = &s_yd[buf][0];
 #pragma unroll
     for (int k = 0; k < 16; k++) {
-      const int m = mt * 32 + 8 * (k >> 2) + 4 * hh + (k & 3);
-      run[k] = run[k] + (c * s_yd[sbb][m]) * acc[k];
-    }
-    int cc = s_fold[i];
-    if (cc >= 0) {  // the finished lane class joins the butterfly tree
-      fold_class(cc, run, h0, h1, l2a);
-      zero16(run);
-      // classes with no superblock (nb < 8) that follow it join as zeros
-      while (++cc < 8 && class_len(cc, nb) == 0) fold_class(cc, run, h0, h1, l2a);
+      const int m = 8 * (k >> 2) + 4 * kh + (k & 3);
+      const float y0 = yd[m], y1 = yd[32 + m];
+      rg0[k] = rg0[k] + (cg * y0) * ag0[k];
+      ru0[k] = ru0[k] + (cu * y0) * au0[k];
+      rg1[k] = rg1[k] + (cg * y1) * ag1[k];
+      ru1[k] = ru1[k] + (cu * y1) * au1[k];
     }
   };
 
-  // --- pipeline: superblock index i uses raw set (i & 1) ---------------------
-  // Loads past the end re-read superblock s_seq[0] and are never used:
-  // unconditional loads keep the wait counts exact.  Each trip covers two
-  // superblocks (nb is even: d is a multiple of 512).
-  GuRaw rx, ry;
-  issue_raw(s_seq[0], rx);
-  issue_raw(s_seq[1], ry);
-  issue_a(s_seq[0], 0);
-  issue_a(s_seq[0], 1);
-  commit(0, 0, s_seq[0], 0, rx);
-  issue_a(s_seq[1], 0);
-  __syncthreads();
-  for (int i = 0; i < nb; i += 2) {
-    const int b0 = s_seq[i], b1 = s_seq[i + 1];
-    const bool more = i + 2 < nb;
-    const int b2 = more ? s_seq[i + 2] : b0;
-    const int b3 = more ? s_seq[i + 3] : b0;
-    // stage (b0, 0) in buffer 0
-    mfma_h0();
-    commit(1, 0, b0, 1, rx);
-    issue_a(b1, 1);
-    issue_raw(b2, rx);
+  uint32_t gE[17], uE[17], gO[17], uO[17];
+  load17(raw_at(grow, 0), gE);
+  load17(raw_at(urow, 0), uE);
+  issue_a(0, 0);
+  for (int b = 0; b < nb; b += 2) {  // nb is even (d is a multiple of 512)
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    // stage (b0, 1) in buffer 1
-    mfma_h1();
-    commit(0, 1, b1, 0, ry);
-    issue_a(b2, 0);
-    epilogue(i);
+    issue_a(b + 1, 1);
+    load17(raw_at(grow, b + 1), gO);
+    load17(raw_at(urow, b + 1), uO);
+    superblock(std::true_type{}, 0, gE, uE);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    // stage (b1, 0) in buffer 0
-    mfma_h0();
-    commit(1, 1, b1, 1, ry);
-    issue_a(b2, 1);
-    issue_raw(b3, ry);
-    __syncthreads();
-    // stage (b1, 1) in buffer 1
-    mfma_h1();
-    if (more) commit(0, 0, b2, 0, rx);
-    issue_a(b3, 0);
-    epilogue(i + 1);
-    __syncthreads();
+    if (b + 2 < nb) {
+      issue_a(b + 2, 0);
+      load17(raw_at(grow, b + 2), gE);
+      load17(raw_at(urow, b + 2), uE);
+    }
+    superblock(std::false_type{}, 1, gO, uO);
   }
-#undef DSM_GU_ISSUE_A
 
-  // --- SwiGLU: up rows (waves 2, 3) hand their sums to the gate waves ------
-  float* s_up = (float*)&sA[0][0][0];  // [64 pairs][32 rows] (8 KB of the 16 KB buffer)
-  if (mat == 1) {
+  // SwiGLU (utils.rs:141-163) and the routing weight; rows of dead pairs are not stored
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++) {
 #pragma unroll
     for (int k = 0; k < 16; k++) {
-      const int m = mt * 32 + 8 * (k >> 2) + 4 * hh + (k & 3);
-      s_up[m * kGuBN + (lane & 31)] = h0[k];
-    }
-  }
-  __syncthreads();
-  if (mat == 0) {
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-      const int m = mt * 32 + 8 * (k >> 2) + 4 * hh + (k & 3);
+      const int m = 32 * mt + 8 * (k >> 2) + 4 * kh + (k & 3);
       if (m >= cnt) continue;
       const uint32_t pair = s_pair[m];
-      const float g = clamp_gate(h0[k], a.clamp), u = clamp_up(s_up[m * kGuBN + (lane & 31)], a.clamp);
+      const float g = clamp_gate(mt ? rg1[k] : rg0[k], a.clamp), u = clamp_up(mt ? ru1[k] : ru0[k], a.clamp);
       const float wgt = a.weights ? a.weights[pair] : 1.0f;
-      a.mid[(size_t)pair * I + n0 + (lane & 31)] = (g / (1.0f + expf_dsm(-g))) * u * wgt;
+      a.mid[(size_t)pair * I + n0 + 32 * w + l32] = (g / (1.0f + expf_dsm(-g))) * u * wgt;
     }
   }
 }

@@ -200,9 +200,12 @@ int dsmoe_gate_up_mid(const void* gate, const void* up, const void* xq, const in
 /* moe_gate_up_mid_sorted_qwarp32 (engine/src/kernels/moe.rs:721-815):
  * the pairs grouped by expert by dsmoe_dispatch with block_m =
  * DSMOE_GROUPED_TILE_M; mid_out[pair][row] as dsmoe_gate_up_mid computes it
- * (same bits).  xh/xq: Q8_K(x) from dsmoe_q8k_quantize_h.  weights: routing
+ * up to f32 rounding of the order in which a row's superblock values are
+ * added (superblocks in order here, per-lane partials and a butterfly in the
+ * reference; each superblock's integer sum and block value are the
+ * reference's).  xh/xq: Q8_K(x) from dsmoe_q8k_quantize_h.  weights: routing
  * weight per pair (NULL = 1).  Runs on the matrix cores (f16 operands holding
- * the exact integer codes, f32 accumulation). */
+ * the exact integer codes, f32 accumulation); I a multiple of 256. */
 #define DSMOE_GROUPED_TILE_M 64
 int dsmoe_gate_up_mid_sorted(const void* gate, const void* up, const uint16_t* xh, const void* xq,
                              const uint32_t* sorted_pairs, const uint32_t* offsets, const uint32_t* tile_offsets,
