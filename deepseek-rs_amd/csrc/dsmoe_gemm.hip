@@ -195,6 +195,9 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
   __shared__ __align__(16) u32x4 sA[2][kGuBM * 32];
   __shared__ __align__(16) float s_yd[2][kGuBM];
   __shared__ Iq2HalfTables tab;
+  // the f16 grid table in 16 copies, entry g of copy p at 16 g + p: the 16
+  // lanes of one LDS pass (lane % 16 = p) each read their own bank group
+  __shared__ u32x4 s_grid16[256 * 16];
   __shared__ uint32_t s_pair[kGuBM], s_xrow[kGuBM], s_qrow[kGuBM];
 
   const TileSlab ts = xcd_tile_slab((int)a.tile_offsets[a.E], a.I / kGuBN);
@@ -217,6 +220,12 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
   }
   load_iq2_half_tables(&tab);
   __syncthreads();
+  for (int i = tid; i < 256 * 16; i += 256) {
+    const uint4 g = tab.gridh[i >> 4];
+    s_grid16[i] = u32x4{g.x, g.y, g.z, g.w};
+  }
+  __syncthreads();
+  const u32x4* grid16 = &s_grid16[lane & 15];
 
   // A: wave w's eight loads per superblock fill slots (8w + j) * 64 + lane
   uint32_t aoff[8];
@@ -271,8 +280,9 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
       const uint32_t sh0 = 16 * (ks & 1) + 8 * kh, sh1 = 14 * (ks & 1) + 7 * kh;
       const uint32_t gg = __builtin_amdgcn_ubfe(qs(gr, 2 * sb), sh0, 8), gs = __builtin_amdgcn_ubfe(g1, sh1, 7);
       const uint32_t ug = __builtin_amdgcn_ubfe(qs(ur, 2 * sb), sh0, 8), us = __builtin_amdgcn_ubfe(u1, sh1, 7);
-      const half8 bg = __builtin_bit_cast(half8, iq2_half8(tab.gridh[gg], tab.sign[gs], lsg));
-      const half8 bu = __builtin_bit_cast(half8, iq2_half8(tab.gridh[ug], tab.sign[us], lsu));
+      const u32x4 gv = grid16[16 * gg], uv = grid16[16 * ug];
+      const half8 bg = __builtin_bit_cast(half8, iq2_half8(make_uint4(gv.x, gv.y, gv.z, gv.w), tab.sign[gs], lsg));
+      const half8 bu = __builtin_bit_cast(half8, iq2_half8(make_uint4(uv.x, uv.y, uv.z, uv.w), tab.sign[us], lsu));
       const int c = (2 * ks + kh) ^ l32;
       const half8 a0 = __builtin_bit_cast(half8, sa[l32 * 32 + c]);
       const half8 a1 = __builtin_bit_cast(half8, sa[(32 + l32) * 32 + c]);
