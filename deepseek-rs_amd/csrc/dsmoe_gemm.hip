@@ -149,11 +149,12 @@ __device__ __forceinline__ TileSlab xcd_slab_tile(int ntiles, int ny) { return x
 
 // ---------------------------------------------------------------------------
 // Routed gate/up/SwiGLU over sorted pairs (moe_gate_up_mid_sorted_qwarp32,
-// moe.rs:721-815; per-pair arithmetic of moe.rs:622-715).  A workgroup is one
-// dispatch tile (up to kGuBM = 64 pairs of one expert) x kGuBN = 128 rows of
-// gate and the same rows of up.  Wave w takes rows n0 + 32w .. +31 of gate and
-// of up for all 64 pairs: four 32x32 MFMA tiles (pairs 0-31 / 32-63 x gate /
-// up), so the SwiGLU needs no exchange between waves.
+// moe.rs:721-815; per-pair arithmetic of moe.rs:622-715).  A workgroup of
+// kGuThreads = 512 is one dispatch tile (up to kGuBM = 64 pairs of one expert)
+// x kGuBN = 256 rows of gate and the same rows of up.  Wave w takes rows
+// n0 + 32w .. +31 of gate and of up for all 64 pairs: four 32x32 MFMA tiles
+// (pairs 0-31 / 32-63 x gate / up), so the SwiGLU needs no exchange between
+// waves; with 8 waves (2 per SIMD) the activation tile serves 8 waves.
 //
 // A (the pairs' Q8_K integers as f16): one superblock (64 x 256) per LDS
 // buffer, two buffers, loaded straight into LDS (global_load_lds_dwordx4):
@@ -190,7 +191,7 @@ __device__ __forceinline__ void load17(const uint8_t* p, uint32_t* r) {
 }
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256)
+extern "C" __global__ __launch_bounds__(kGuThreads)
 void dsmoe_gu_grouped(const GuGroupedArgs a) {
   __shared__ __align__(16) u32x4 sA[2][kGuBM * 32];
   __shared__ __align__(16) float s_yd[2][kGuBM];
@@ -220,26 +221,27 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
   }
   load_iq2_half_tables(&tab);
   __syncthreads();
-  for (int i = tid; i < 256 * 16; i += 256) {
+  for (int i = tid; i < 256 * 16; i += kGuThreads) {
     const uint4 g = tab.gridh[i >> 4];
     s_grid16[i] = u32x4{g.x, g.y, g.z, g.w};
   }
   __syncthreads();
   const u32x4* grid16 = &s_grid16[lane & 15];
 
-  // A: wave w's eight loads per superblock fill slots (8w + j) * 64 + lane
-  uint32_t aoff[8];
+  // A: wave w's loads per superblock fill slots (kAj w + j) * 64 + lane
+  constexpr int kAj = 2048 / 64 / (kGuThreads / 64);
+  uint32_t aoff[kAj];
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const int sl = (8 * w + j) * 64 + lane, m = sl >> 5, c = (sl & 31) ^ (m & 31);
+  for (int j = 0; j < kAj; j++) {
+    const int sl = (kAj * w + j) * 64 + lane, m = sl >> 5, c = (sl & 31) ^ (m & 31);
     aoff[j] = s_xrow[m] + 16u * (uint32_t)c;
   }
   const uint32_t qoff = s_qrow[lane];
   auto issue_a = [&](int b, int buf) {
     const uint8_t* base = (const uint8_t*)a.xh + 512 * b;
 #pragma unroll
-    for (int j = 0; j < 8; j++)
-      __builtin_amdgcn_global_load_lds((glb_void*)(base + aoff[j]), (lds_void*)&sA[buf][(8 * w + j) * 64], 16, 0, 0);
+    for (int j = 0; j < kAj; j++)
+      __builtin_amdgcn_global_load_lds((glb_void*)(base + aoff[j]), (lds_void*)&sA[buf][(kAj * w + j) * 64], 16, 0, 0);
     if (w == 0)  // the 64 pairs' block scales: lane l -> s_yd[buf][l]
       __builtin_amdgcn_global_load_lds((glb_void*)(a.xq + qoff + (size_t)b * Q8K_BYTES), (lds_void*)&s_yd[buf][0], 4,
                                        0, 0);
@@ -257,11 +259,19 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
 
   // one superblock from LDS buffer buf and raw rows gr / ur (kEven: the qs
   // start 2 bytes into the loaded words)
-  auto superblock = [&](auto even_tag, int buf, const uint32_t* gr, const uint32_t* ur) {
+  auto superblock = [&](auto even_tag, int buf, uint32_t* gr, uint32_t* ur) {
     constexpr bool kEven = decltype(even_tag)::value;
-    auto qs = [&](const uint32_t* r, int j) -> uint32_t {
-      return kEven ? __builtin_amdgcn_alignbyte(r[j + 1], r[j], 2) : r[j + 1];
-    };
+    // the block scale, then the qs words realigned in place (even superblocks
+    // start 2 bytes into the loaded words): qs word j is r[j + 1]
+    const uint32_t dg = kEven ? gr[0] & 0xFFFF : gr[0] >> 16, du = kEven ? ur[0] & 0xFFFF : ur[0] >> 16;
+    if (kEven) {
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        gr[j] = __builtin_amdgcn_alignbyte(gr[j + 1], gr[j], 2);
+        ur[j] = __builtin_amdgcn_alignbyte(ur[j + 1], ur[j], 2);
+      }
+    }
+    auto qs = [&](const uint32_t* r, int j) -> uint32_t { return kEven ? r[j] : r[j + 1]; };
     float16v ag0, ag1, au0, au1;
 #pragma unroll
     for (int i = 0; i < 16; i++) { ag0[i] = 0.0f; ag1[i] = 0.0f; au0[i] = 0.0f; au1[i] = 0.0f; }
@@ -292,17 +302,17 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
       au1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bu, au1, 0, 0, 0);
     }
     // block values 0.125 * xd * yd * sum (quantize.rs:763-812), added in superblock order
-    const float cg = 0.125f * f16_to_f32_ftz((uint16_t)(kEven ? gr[0] & 0xFFFF : gr[0] >> 16));
-    const float cu = 0.125f * f16_to_f32_ftz((uint16_t)(kEven ? ur[0] & 0xFFFF : ur[0] >> 16));
+    const float cg = 0.125f * f16_to_f32_ftz((uint16_t)dg);
+    const float cu = 0.125f * f16_to_f32_ftz((uint16_t)du);
     const float* yd = &s_yd[buf][0];
 #pragma unroll
     for (int k = 0; k < 16; k++) {
       const int m = 8 * (k >> 2) + 4 * kh + (k & 3);
       const float y0 = yd[m], y1 = yd[32 + m];
-      rg0[k] = rg0[k] + (cg * y0) * ag0[k];
-      ru0[k] = ru0[k] + (cu * y0) * au0[k];
-      rg1[k] = rg1[k] + (cg * y1) * ag1[k];
-      ru1[k] = ru1[k] + (cu * y1) * au1[k];
+      rg0[k] = __builtin_fmaf(cg * y0, ag0[k], rg0[k]);
+      ru0[k] = __builtin_fmaf(cu * y0, au0[k], ru0[k]);
+      rg1[k] = __builtin_fmaf(cg * y1, ag1[k], rg1[k]);
+      ru1[k] = __builtin_fmaf(cu * y1, au1[k], ru1[k]);
     }
   };
 

@@ -610,13 +610,13 @@ int dsmoe_gate_up_mid_sorted(const void* gate, const void* up, const uint16_t* x
   if (!aligned16(gate) || !aligned16(up) || !aligned16(xh))
     return fail(DSMOE_ERR_INVALID, "gate_up_mid_sorted: weights and xh must be 16-byte aligned");
   if (d <= 0 || d % 512 || d > 8192) return fail(DSMOE_ERR_UNSUPPORTED, "gate_up_mid_sorted: d must be a multiple of 512, <= 8192");
-  if (I <= 0 || I % 256 || k <= 0 || E <= 0 || pairs < 0) return fail(DSMOE_ERR_INVALID, "gate_up_mid_sorted: bad shape");
+  if (I <= 0 || I % kGuBN || k <= 0 || E <= 0 || pairs < 0) return fail(DSMOE_ERR_INVALID, "gate_up_mid_sorted: bad shape");
   if (pairs == 0) return DSMOE_OK;
   GuGroupedArgs a{(const uint8_t*)gate, (const uint8_t*)up, xh, (const uint8_t*)xq, sorted_pairs, offsets,
                   tile_offsets, tile_experts, tile_starts, weights, mid_out, d, I, k, E, clamp};
   // tiles per expert <= ceil(count / BM): at most pairs / BM + one partial tile per used expert
   const int max_tiles = pairs / kGuBM + std::min(E, pairs);
-  return launch(K_GU_GROUPED, dim3(xcd_grid(max_tiles, I / kGuBN)), dim3(256), 0, stream, a);
+  return launch(K_GU_GROUPED, dim3(xcd_grid(max_tiles, I / kGuBN)), dim3(kGuThreads), 0, stream, a);
 }
 
 int dsmoe_down_sorted(const void* down, const uint16_t* mh, const void* mq, const uint32_t* sorted_pairs,

@@ -204,7 +204,7 @@ struct GuGroupedArgs {
   int32_t d, I, k, E;
   float clamp;
 };
-enum : int32_t { kGuBM = 64, kGuBN = 128 };
+enum : int32_t { kGuBM = 64, kGuThreads = 512, kGuBN = kGuThreads / 2 };
 
 // Grouped routed down projection (Q2_K) over sorted pairs: one workgroup =
 // up to kGuBM pairs of one expert x kDnBN output rows; writes the per-pair
