@@ -199,6 +199,8 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
   // the f16 grid table in 16 copies, entry g of copy p at 16 g + p: the 16
   // lanes of one LDS pass (lane % 16 = p) each read their own bank group
   __shared__ u32x4 s_grid16[256 * 16];
+  // the sign masks in 8 copies (entry i of copy p at 8 i + p, p = lane % 8)
+  __shared__ u32x4 s_sign8[128 * 8];
   __shared__ uint32_t s_pair[kGuBM], s_xrow[kGuBM], s_qrow[kGuBM];
 
   const TileSlab ts = xcd_tile_slab((int)a.tile_offsets[a.E], a.I / kGuBN);
@@ -226,7 +228,13 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
     s_grid16[i] = u32x4{g.x, g.y, g.z, g.w};
   }
   __syncthreads();
+  for (int i = tid; i < 128 * 8; i += kGuThreads) {
+    const uint4 g = tab.sign[i >> 3];
+    s_sign8[i] = u32x4{g.x, g.y, g.z, g.w};
+  }
+  __syncthreads();
   const u32x4* grid16 = &s_grid16[lane & 15];
+  const u32x4* sign8 = &s_sign8[lane & 7];
 
   // A: wave w's loads per superblock fill slots (kAj w + j) * 64 + lane
   constexpr int kAj = 2048 / 64 / (kGuThreads / 64);
@@ -291,8 +299,11 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
       const uint32_t gg = __builtin_amdgcn_ubfe(qs(gr, 2 * sb), sh0, 8), gs = __builtin_amdgcn_ubfe(g1, sh1, 7);
       const uint32_t ug = __builtin_amdgcn_ubfe(qs(ur, 2 * sb), sh0, 8), us = __builtin_amdgcn_ubfe(u1, sh1, 7);
       const u32x4 gv = grid16[16 * gg], uv = grid16[16 * ug];
-      const half8 bg = __builtin_bit_cast(half8, iq2_half8(make_uint4(gv.x, gv.y, gv.z, gv.w), tab.sign[gs], lsg));
-      const half8 bu = __builtin_bit_cast(half8, iq2_half8(make_uint4(uv.x, uv.y, uv.z, uv.w), tab.sign[us], lsu));
+      const u32x4 gsv = sign8[8 * gs], usv = sign8[8 * us];
+      const half8 bg = __builtin_bit_cast(half8, iq2_half8(make_uint4(gv.x, gv.y, gv.z, gv.w),
+                                                           make_uint4(gsv.x, gsv.y, gsv.z, gsv.w), lsg));
+      const half8 bu = __builtin_bit_cast(half8, iq2_half8(make_uint4(uv.x, uv.y, uv.z, uv.w),
+                                                           make_uint4(usv.x, usv.y, usv.z, usv.w), lsu));
       const int c = (2 * ks + kh) ^ l32;
       const half8 a0 = __builtin_bit_cast(half8, sa[l32 * 32 + c]);
       const half8 a1 = __builtin_bit_cast(half8, sa[(32 + l32) * 32 + c]);
