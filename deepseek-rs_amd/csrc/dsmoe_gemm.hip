@@ -364,26 +364,63 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Routed down projection over sorted pairs (moe_down_sorted_qwarp32 /
-// moe_down_qwarp32, moe.rs:821-916; block arithmetic quantize.rs:846-901).
-// Per superblock: isum = sum_k (sc_lo * q)[n][k] * q8[m][k] (weights 0..45 in
-// f16, |isum| < 2^21) and summs = sum_j bsums[m][j] * sc_hi[n][j] (a K = 16
-// product), both exact in f32; then dall * isum - dmin' * summs with
-// dall = yd * d, dmin' = yd * dmin, and the per-pair row sum over
-// superblocks in the reference's 8-lane order.  The slot sum is moe_sum.
-// grid = 8 * ceil(max tiles / 8) * (d / kDnBN) (xcd_tile_slab), 256 threads: wave w computes pairs
-// 32*(w&1).. x rows 32*(w>>1)..
+// Routed down projection over sorted pairs, weights in registers
+// (moe_down_sorted_qwarp32, moe.rs:871-916; block arithmetic
+// quantize.rs:846-901).  A workgroup of 512 is one dispatch tile (up to
+// kGuBM = 64 pairs of one expert) x kDnBN = 256 output rows; wave w computes
+// all 64 pairs x rows n0 + 32w .. +31 as two 32x32 MFMA tiles (small enough
+// for two workgroups, 4 waves per SIMD).
+//
+// Per superblock: isum = sum_k (sc * q)[n][k] * q8[m][k] on the matrix cores
+// (weights sc * q <= 45 as exact f16, each lane building its own row's
+// operand: 8 two-bit codes -> (1024 + q) as f16 bytes by v_perm, then one
+// packed f16 fma (1024 + q) * sc - 1024 * sc = q * sc, exact), then
+// summs = sum_j bsums[m][j] * min_j[n] as one K = 16 MFMA into the same
+// accumulators; the row sum gets yd * d * isum - yd * dmin * summs, the
+// superblocks of a row in order 0, 1, ... (the reference: per-lane partials
+// and a butterfly; f32 rounding of that order).  Activations (the mid codes
+// as f16) come through LDS one superblock per buffer (direct-to-LDS loads),
+// with the block scales and bsums.
 // ---------------------------------------------------------------------------
-extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+namespace {
+// 13 words of a Q2_K row's superblock for lane half kh: the scales (words
+// 0-3), the code bytes 16 + 8 kh + 16 p (p = 0..3: words 4 + 2p, 5 + 2p) and
+// d | dmin (word 12)
+__device__ __forceinline__ void load_q2(const uint8_t* blk, int kh, uint32_t* r) {
+  const u32x4 s4 = *(const u32x4*)blk;
+  r[0] = s4.x; r[1] = s4.y; r[2] = s4.z; r[3] = s4.w;
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    const uint2 v = *(const uint2*)(blk + 16 + 8 * kh + 16 * p);
+    r[4 + 2 * p] = v.x;
+    r[5 + 2 * p] = v.y;
+  }
+  r[12] = *(const uint32_t*)(blk + 80);
+}
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+// 8 codes (bytes of w0, w1 after shift and mask) times the group scale as f16
+__device__ __forceinline__ half8 q2_half8(uint32_t w0, uint32_t w1, uint32_t shift, half2v sc2, half2v off2) {
+  const uint32_t b0 = (w0 >> shift) & 0x03030303u, b1 = (w1 >> shift) & 0x03030303u;
+  // bytes (q_a, 0x64, q_b, 0x64) are the f16 values 1024 + q; one fused
+  // (1024 + q) * sc - 1024 * sc rounds once, from the exact q * sc
+  auto cv = [&](uint32_t x) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2v, x), sc2, off2));
+  };
+  u32x4 v;
+  v.x = cv(__builtin_amdgcn_perm(0x64646464u, b0, 0x04010400u));
+  v.y = cv(__builtin_amdgcn_perm(0x64646464u, b0, 0x04030402u));
+  v.z = cv(__builtin_amdgcn_perm(0x64646464u, b1, 0x04010400u));
+  v.w = cv(__builtin_amdgcn_perm(0x64646464u, b1, 0x04030402u));
+  return __builtin_bit_cast(half8, v);
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(kDnThreads)
 void dsmoe_dn_grouped(const DnGroupedArgs a) {
-  // A: row-major [pair][32 chunks], chunk XOR-swizzled by (row & 15)
-  // B: chunk-major [32 chunks][64 rows], row slot XOR-swizzled by 2 * (chunk / 8)
-  __shared__ uint4 sA[kGuBM][32];
-  __shared__ uint4 sB[32][kDnBN];
-  __shared__ __align__(16) _Float16 sBS[kGuBM][16];  // bsums
-  __shared__ __align__(16) _Float16 sM[kDnBN][16];   // sc >> 4
-  __shared__ float s_yd[kGuBM], s_d[kDnBN], s_dmin[kDnBN];
-  __shared__ uint32_t s_pair[kGuBM];
+  __shared__ __align__(16) u32x4 sA[2][kGuBM * 32];    // mid codes, slot m * 32 + (c ^ (m & 31))
+  __shared__ __align__(16) u32x4 sBS[2][kGuBM * 2];    // bsums (int16), two 16-byte halves per pair
+  __shared__ __align__(16) float s_yd[2][kGuBM];
+  __shared__ uint32_t s_pair[kGuBM], s_mrow[kGuBM], s_qrow[kGuBM];
 
   const TileSlab ts = xcd_tile_slab((int)a.tile_offsets[a.E], a.d / kDnBN);
   if (!ts.ok) return;
@@ -392,163 +429,149 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
   const int p0 = (int)(a.offsets[e] + a.tile_starts[t]);
   const int cnt = min(kGuBM, (int)a.offsets[e + 1] - p0);
   const int n0 = ts.n * kDnBN;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, kh = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int d = a.d, I = a.I, nb = I >> 8;
 
-  if (tid < kGuBM) s_pair[tid] = tid < cnt ? a.sorted_pairs[p0 + tid] : 0xFFFFFFFFu;
+  if (tid < kGuBM) {
+    const uint32_t pr = tid < cnt ? a.sorted_pairs[p0 + tid] : 0xFFFFFFFFu;
+    const uint32_t row = pr != 0xFFFFFFFFu ? pr : 0u;  // dead rows read pair 0, never stored
+    s_pair[tid] = pr;
+    s_mrow[tid] = row * (uint32_t)I * 2u;
+    s_qrow[tid] = row * (uint32_t)nb * (uint32_t)Q8K_BYTES;
+  }
   __syncthreads();
-
-  // Wave w owns rows 16w .. 16w+15 of both operands; lane l handles row
-  // 16w + l/4, quarter p = l % 4 (elements 64p .. 64p+63 of a superblock).
-  // Dead pair rows read pair 0: finite, never stored.
-  const int r = 16 * w + (lane >> 2), pq = lane & 3;
-  // activation loads: instruction j covers rows 16w + 2j + lane/32, chunk lane % 32
-  uint32_t aoff[8];
+  // A: 2048 slots of 16 bytes per superblock, four loads per wave
+  uint32_t aoff[4];
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const uint32_t pr = s_pair[16 * w + 2 * j + (lane >> 5)];
-    aoff[j] = (pr != 0xFFFFFFFFu ? pr : 0u) * (uint32_t)I + 8 * (lane & 31);
+  for (int j = 0; j < 4; j++) {
+    const int sl = (4 * w + j) * 64 + lane, m = sl >> 5, c = (sl & 31) ^ (m & 31);
+    aoff[j] = s_mrow[m] + 16u * (uint32_t)c;
   }
-  const uint32_t mpair = s_pair[r] != 0xFFFFFFFFu ? s_pair[r] : 0u;
-  const uint8_t* mrow = a.mq + (size_t)mpair * nb * Q8K_BYTES;
-  const uint8_t* wrow = a.down + ((size_t)e * d + n0 + r) * nb * Q2K_BYTES;
-
-  // named registers: an array captured by the lambdas ends up in scratch
-  uint4 av0, av1, av2, av3, av4, av5, av6, av7;
-  uint32_t abs0, abs1, bsc, bdd;
-  uint4 bq0, bq1;
-  float ayd;
-  auto issue = [&](int b) {
-    const uint16_t* base = a.mh + 256 * b;
-    av0 = *(const uint4*)(base + aoff[0]);
-    av1 = *(const uint4*)(base + aoff[1]);
-    av2 = *(const uint4*)(base + aoff[2]);
-    av3 = *(const uint4*)(base + aoff[3]);
-    av4 = *(const uint4*)(base + aoff[4]);
-    av5 = *(const uint4*)(base + aoff[5]);
-    av6 = *(const uint4*)(base + aoff[6]);
-    av7 = *(const uint4*)(base + aoff[7]);
-    const uint8_t* mb = mrow + (size_t)b * Q8K_BYTES;
-    ayd = ld_f32(mb);
-    abs0 = *(const uint32_t*)(mb + 260 + 8 * pq);
-    abs1 = *(const uint32_t*)(mb + 264 + 8 * pq);
-    const uint32_t* blk = (const uint32_t*)(wrow + (size_t)b * Q2K_BYTES);
-    bsc = blk[pq];                                      // scales of groups 4p .. 4p+3
-    bq0 = *(const uint4*)(blk + 4 + 8 * (pq >> 1));     // qs half p / 2 (32 bytes)
-    bq1 = *(const uint4*)(blk + 8 + 8 * (pq >> 1));
-    bdd = blk[20];                                      // d | dmin
+  // wave 0: block scales (lane = pair); waves 1, 2: bsums halves (lane = pair)
+  const uint32_t qoff = s_qrow[lane] + (w == 0 ? 0u : 260u + 16u * (uint32_t)(w - 1));
+  auto issue_a = [&](int b, int buf) {
+    const uint8_t* base = (const uint8_t*)a.mh + 512 * b;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      __builtin_amdgcn_global_load_lds((glb_void*)(base + aoff[j]), (lds_void*)&sA[buf][(4 * w + j) * 64], 16, 0, 0);
+    if (w == 0)
+      __builtin_amdgcn_global_load_lds((glb_void*)(a.mq + qoff + (size_t)b * Q8K_BYTES), (lds_void*)&s_yd[buf][0], 4,
+                                       0, 0);
+    else if (w < 3)
+      __builtin_amdgcn_global_load_lds((glb_void*)(a.mq + qoff + (size_t)b * Q8K_BYTES),
+                                       (lds_void*)&sBS[buf][64 * (w - 1)], 16, 0, 0);
   };
-  auto commit = [&]() {
-#define DSM_STORE_A(j, v)                            \
-    {                                                \
-      const int row = 16 * w + 2 * (j) + (lane >> 5); \
-      sA[row][(lane & 31) ^ (row & 15)] = v;         \
-    }
-    DSM_STORE_A(0, av0)
-    DSM_STORE_A(1, av1)
-    DSM_STORE_A(2, av2)
-    DSM_STORE_A(3, av3)
-    DSM_STORE_A(4, av4)
-    DSM_STORE_A(5, av5)
-    DSM_STORE_A(6, av6)
-    DSM_STORE_A(7, av7)
-#undef DSM_STORE_A
-    {
-      typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-      const h4 v = {(_Float16)(float)(int16_t)(abs0 & 0xFFFF), (_Float16)(float)(int16_t)(abs0 >> 16),
-                    (_Float16)(float)(int16_t)(abs1 & 0xFFFF), (_Float16)(float)(int16_t)(abs1 >> 16)};
-      *(h4*)&sBS[r][4 * pq] = v;
-      const h4 m = {(_Float16)(float)((bsc >> 4) & 0xF), (_Float16)(float)((bsc >> 12) & 0xF),
-                    (_Float16)(float)((bsc >> 20) & 0xF), (_Float16)(float)((bsc >> 28) & 0xF)};
-      *(h4*)&sM[r][4 * pq] = m;
-    }
-    if (pq == 0) {
-      s_yd[r] = ayd;
-      s_d[r] = f16_to_f32_ftz((uint16_t)(bdd & 0xFFFF));
-      s_dmin[r] = f16_to_f32_ftz((uint16_t)(bdd >> 16));
-    }
-    const uint32_t bqs[8] = {bq0.x, bq0.y, bq0.z, bq0.w, bq1.x, bq1.y, bq1.z, bq1.w};
-    const int slot = r ^ (2 * pq);
-    // weights sc_lo * q as f16: each group's values {0, L, 2L, 3L} are a
-    // 4-entry table that v_perm indexes with the 2-bit codes
+  const size_t rb = (size_t)nb * Q2K_BYTES;
+  const uint8_t* row0 = a.down + ((size_t)e * d + n0 + 32 * w + l32) * rb;
+
+  float16v run[2];  // pair tiles 0-31, 32-63
 #pragma unroll
-    for (int s2 = 0; s2 < 2; s2++) {
-      const uint32_t shift = 2 * (2 * (pq & 1) + s2);
+  for (int q = 0; q < 2; q++)
 #pragma unroll
-      for (int gh = 0; gh < 2; gh++) {  // the two 16-element groups of this 32-element run
-        const uint32_t L = (bsc >> (8 * (2 * s2 + gh))) & 0xF;
-        const uint32_t t_lo = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)L) << 16;
-        const uint32_t t_hi = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)(2 * L)) |
-                              ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)(3 * L)) << 16);
-        uint32_t o[8];
+    for (int i = 0; i < 16; i++) run[q][i] = 0.0f;
+
+  auto superblock = [&](int buf, const uint32_t* r0) {
+    float16v acc[2];
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++) {
-          const uint32_t qb = (bqs[4 * gh + tt] >> shift) & 0x03030303u;
-          const uint32_t x01 = __builtin_amdgcn_perm(0u, qb, 0x0c010c00u), x23 = __builtin_amdgcn_perm(0u, qb, 0x0c030c02u);
-          o[2 * tt] = __builtin_amdgcn_perm(t_hi, t_lo, x01 * 0x0202u + 0x01000100u);
-          o[2 * tt + 1] = __builtin_amdgcn_perm(t_hi, t_lo, x23 * 0x0202u + 0x01000100u);
-        }
-        const int c = 8 * pq + 4 * s2 + 2 * gh;  // elements 8c .. 8c+15
-        sB[c][slot] = make_uint4(o[0], o[1], o[2], o[3]);
-        sB[c + 1][slot] = make_uint4(o[4], o[5], o[6], o[7]);
-      }
+    for (int q = 0; q < 2; q++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc[q][i] = 0.0f;
+    const u32x4* sa = &sA[buf][0];
+#pragma unroll
+    for (int ks = 0; ks < 16; ks++) {
+      // group ks: codes at piece 2 (ks >> 3) + (ks & 1), shift 2 ((ks & 7) >> 1)
+      const int pc = 2 * (ks >> 3) + (ks & 1);
+      const uint32_t shift = 2 * ((ks & 7) >> 1);
+      const uint32_t s0 = (r0[ks >> 2] >> (8 * (ks & 3))) & 0xF;
+      const _Float16 f0 = (_Float16)(float)s0;
+      const half2v sc0 = {f0, f0};
+      const half2v of0 = {(_Float16)(-1024.0f) * f0, (_Float16)(-1024.0f) * f0};
+      const half8 b0 = q2_half8(r0[4 + 2 * pc], r0[5 + 2 * pc], shift, sc0, of0);
+      const int c = (2 * ks + kh) ^ l32;
+      const half8 a0 = __builtin_bit_cast(half8, sa[l32 * 32 + c]);
+      const half8 a1 = __builtin_bit_cast(half8, sa[(32 + l32) * 32 + c]);
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b0, acc[1], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);  // one k-step's operands live at a time
+    }
+    // isum part: + yd * d * isum
+    const float* yd = &s_yd[buf][0];
+    const float dn0 = f16_to_f32_ftz((uint16_t)(r0[12] & 0xFFFF)), dm0 = f16_to_f32_ftz((uint16_t)(r0[12] >> 16));
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const int m = 8 * (k >> 2) + 4 * kh + (k & 3);
+      run[0][k] = __builtin_fmaf(yd[m] * dn0, acc[0][k], run[0][k]);
+      run[1][k] = __builtin_fmaf(yd[32 + m] * dn0, acc[1][k], run[1][k]);
+    }
+    // summs = bsums . min over the 16 groups: one K = 16 product per tile
+    // (bsums |.| <= 16 * 128 and the 4-bit mins are exact in f16)
+    auto mins8 = [&](const uint32_t* r) {  // min_j for j = 8 kh .. 8 kh + 7
+      const uint32_t m0 = (r[0 + 2 * kh] >> 4) & 0x0F0F0F0Fu, m1 = (r[1 + 2 * kh] >> 4) & 0x0F0F0F0Fu;
+      const half2v off = {(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
+      auto cv = [&](uint32_t x) { return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, x) + off); };
+      u32x4 v;
+      v.x = cv(__builtin_amdgcn_perm(0x64646464u, m0, 0x04010400u));
+      v.y = cv(__builtin_amdgcn_perm(0x64646464u, m0, 0x04030402u));
+      v.z = cv(__builtin_amdgcn_perm(0x64646464u, m1, 0x04010400u));
+      v.w = cv(__builtin_amdgcn_perm(0x64646464u, m1, 0x04030402u));
+      return __builtin_bit_cast(half8, v);
+    };
+    auto bsums8 = [&](int m) {  // bsums[m][8 kh .. 8 kh + 7] as f16
+      const u32x4 v = sBS[buf][64 * kh + m];
+      auto cv = [](uint32_t x) {
+        const half2v h = {(_Float16)(float)(int16_t)(x & 0xFFFF), (_Float16)(float)(int16_t)(x >> 16)};
+        return __builtin_bit_cast(uint32_t, h);
+      };
+      return __builtin_bit_cast(half8, u32x4{cv(v.x), cv(v.y), cv(v.z), cv(v.w)});
+    };
+    const half8 mn0 = mins8(r0);
+    const half8 bs0 = bsums8(l32), bs1 = bsums8(32 + l32);
+    float16v z;
+#pragma unroll
+    for (int i = 0; i < 16; i++) z[i] = 0.0f;
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bs0, mn0, z, 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bs1, mn0, z, 0, 0, 0);
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const int m = 8 * (k >> 2) + 4 * kh + (k & 3);
+      run[0][k] = __builtin_fmaf(-(yd[m] * dm0), acc[0][k], run[0][k]);
+      run[1][k] = __builtin_fmaf(-(yd[32 + m] * dm0), acc[1][k], run[1][k]);
     }
   };
 
-  const int mt = w & 1, nt = w >> 1, hh = lane >> 5;
-  const int arow_l = mt * 32 + (lane & 31), brow_l = nt * 32 + (lane & 31), koff = 8 * hh;
-  float16v run, h0, h1, l2a;
-  for (int i = 0; i < 16; i++) { run[i] = 0.0f; h0[i] = 0.0f; h1[i] = 0.0f; l2a[i] = 0.0f; }
-  auto block_of = [&](int ci, int j) { return lane_class(ci) + 8 * j; };
-
-  int ci = 0;
-  while (ci < 8 && class_len(ci, nb) == 0) ci++;
-  if (ci < 8) issue(block_of(ci, 0));
-  for (int cc = 0; cc < 8; cc++) {
-    const int len = class_len(cc, nb);
-    for (int jj = 0; jj < len; jj++) {
-      __syncthreads();
-      commit();
-      // the next superblock's loads (unconditional: past the end re-reads
-      // superblock 0, never used; keeps the wait counts exact)
-      int nc = cc, nj = jj + 1;
-      if (nj >= len) {
-        nc = cc + 1;
-        nj = 0;
-        while (nc < 8 && class_len(nc, nb) == 0) nc++;
-      }
-      issue(nc < 8 ? block_of(nc, nj) : 0);
-      __syncthreads();
-      float16v isum, summs;
-      for (int i = 0; i < 16; i++) { isum[i] = 0.0f; summs[i] = 0.0f; }
-#pragma unroll
-      for (int ks = 0; ks < 16; ks++) {
-        const int c = 2 * ks + hh;
-        const half8 av8 = *(const half8*)&sA[arow_l][c ^ (arow_l & 15)];
-        const half8 bv8 = *(const half8*)&sB[c][brow_l ^ (2 * (ks >> 2))];
-        isum = __builtin_amdgcn_mfma_f32_32x32x16_f16(av8, bv8, isum, 0, 0, 0);
-      }
-      summs = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const half8*)&sBS[arow_l][koff],
-                                                      *(const half8*)&sM[brow_l][koff], summs, 0, 0, 0);
-      const float dn = s_d[brow_l], dm = s_dmin[brow_l];
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const int m = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-        const float yd = s_yd[m];
-        const float dall = yd * dn, dmin = yd * dm;
-        run[i] = run[i] + (dall * isum[i] - dmin * summs[i]);
-      }
+  uint32_t e0[13], o0[13];
+  load_q2(row0, kh, e0);
+  issue_a(0, 0);
+  for (int b = 0; b < nb; b += 2) {
+    const bool odd = b + 1 < nb;  // the odd superblock of this pair exists
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (odd) {
+      issue_a(b + 1, 1);
+      load_q2(row0 + (size_t)(b + 1) * Q2K_BYTES, kh, o0);
     }
-    fold_class(cc, run, h0, h1, l2a);
-    for (int i = 0; i < 16; i++) run[i] = 0.0f;
+    superblock(0, e0);
+    if (!odd) break;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (b + 2 < nb) {
+      issue_a(b + 2, 0);
+      load_q2(row0 + (size_t)(b + 2) * Q2K_BYTES, kh, e0);
+    }
+    superblock(1, o0);
   }
+
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const int m = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-    if (m >= cnt) continue;
-    a.down_out[(size_t)s_pair[m] * d + n0 + nt * 32 + (lane & 31)] = h0[i];
-  }
+  for (int q = 0; q < 2; q++)
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const int m = 32 * q + 8 * (k >> 2) + 4 * kh + (k & 3);
+      if (m >= cnt) continue;
+      a.down_out[(size_t)s_pair[m] * d + n0 + 32 * w + l32] = run[q][k];
+    }
 }
+
 
 // ---------------------------------------------------------------------------
 // Shared expert for batches: Q8_0 weights x Q8_0 activations

@@ -632,7 +632,7 @@ int dsmoe_down_sorted(const void* down, const uint16_t* mh, const void* mq, cons
   DnGroupedArgs a{(const uint8_t*)down, mh, (const uint8_t*)mq, sorted_pairs, offsets, tile_offsets, tile_experts,
                   tile_starts, down_out, d, I, E};
   const int max_tiles = pairs / kGuBM + std::min(E, pairs);
-  return launch(K_DN_GROUPED, dim3(xcd_grid(max_tiles, d / kDnBN)), dim3(256), 0, stream, a);
+  return launch(K_DN_GROUPED, dim3(xcd_grid(max_tiles, d / kDnBN)), dim3(kDnThreads), 0, stream, a);
 }
 
 int dsmoe_gate_up_mid_em(const void* gate, const void* up, const void* xq, const uint32_t* sorted_pairs,

@@ -221,7 +221,7 @@ struct DnGroupedArgs {
   float* down_out;                // [P][d]
   int32_t d, I, E;
 };
-enum : int32_t { kDnBN = 64 };
+enum : int32_t { kDnThreads = 512, kDnBN = kDnThreads / 2 };
 
 // Dense Q8_0 x Q8_0-activation GEMM for batches (shared expert): tiles of
 // kGuBM tokens x 64 output columns (32 gate + 32 up rows with SwiGLU, or 64

@@ -238,8 +238,11 @@ int dsmoe_down_em(const void* down, const void* mq, const uint32_t* sorted_pairs
 /* moe_down_sorted_qwarp32 (engine/src/kernels/moe.rs:821-916, sorted
  * variant): down_out[pair][row] for the pairs grouped by dsmoe_dispatch
  * (block_m = DSMOE_GROUPED_TILE_M), the per-pair values dsmoe_down computes
- * (same bits); mh/mq: Q8_K(mid) from dsmoe_q8k_quantize_h.  The slot sum is
- * dsmoe_moe_sum.  Matrix cores, exact integer codes in f16. */
+ * up to f32 rounding of the order in which a row's superblock values are
+ * added (each superblock's integer sums and block value are the
+ * reference's); mh/mq: Q8_K(mid) from dsmoe_q8k_quantize_h.  The slot sum is
+ * dsmoe_moe_sum.  Matrix cores, exact integer codes in f16; d a multiple of
+ * 256. */
 int dsmoe_down_sorted(const void* down, const uint16_t* mh, const void* mq, const uint32_t* sorted_pairs,
                       const uint32_t* offsets, const uint32_t* tile_offsets, const uint32_t* tile_experts,
                       const uint32_t* tile_starts, float* down_out, int32_t d, int32_t I, int32_t E, int32_t pairs,

@@ -246,7 +246,7 @@ def test_gate_up_sorted_matches_per_pair(gpu, d, I, E, T, k, skew, big):
     in order 0, 1, 2, ... where the reference adds per-lane partials and a
     butterfly: the two differ by f32 rounding of that order, bounded here at
     rel-L2 1e-5 and 1e-4 of the row scale per element (north_star allows
-    1e-3).  The grouped down stays bit-exact."""
+    1e-3).  The grouped down the same way against the per-pair down."""
     import torch
     say(f"gate_up sorted d={d} I={I} E={E} T={T} k={k} skew={skew} big={big}")
     rng = np.random.default_rng(d + I + T)
@@ -304,8 +304,12 @@ def test_gate_up_sorted_matches_per_pair(gpu, d, I, E, T, k, skew, big):
     dd = torch.full((P_, d), float("nan"), device=gpu)
     dsmoe.down_sorted(dn, mh, mq, sp, offsets, toff, texp, tst, dd, d, I, E, P_)
     torch.cuda.synchronize()
-    assert_close(np_(dd).reshape(-1), np_(dd_ref).reshape(-1), "down sorted vs per-pair")
-    assert bits_equal(np_(dd), np_(dd_ref))
+    got, want = np_(dd).astype(np.float64), np_(dd_ref).astype(np.float64)
+    assert np.isfinite(got).all()
+    r = rel_l2(got, want)
+    elem = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+    say(f"  down sorted vs per-pair: rel_l2={r:.3e} max_abs/row_scale={elem:.3e}")
+    assert r <= 1e-5 and elem <= 1e-4, (r, elem)
 
 
 @pytest.mark.parametrize("d,I,E,T,k,skew,bm", [(7168, 2048, 16, 40, 8, True, 8), (7168, 2048, 256, 32, 8, False, 2),
