@@ -196,11 +196,11 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
   __shared__ __align__(16) u32x4 sA[2][kGuBM * 32];
   __shared__ __align__(16) float s_yd[2][kGuBM];
   __shared__ Iq2HalfTables tab;
-  // the f16 grid table in 16 copies, entry g of copy p at 16 g + p: the 16
-  // lanes of one LDS pass (lane % 16 = p) each read their own bank group
-  __shared__ u32x4 s_grid16[256 * 16];
-  // the sign masks in 8 copies (entry i of copy p at 8 i + p, p = lane % 8)
-  __shared__ u32x4 s_sign8[128 * 8];
+  // the f16 grid table in 8 copies, entry g of copy p at 8 g + p (p = lane % 8)
+  __shared__ u32x4 s_grid8[256 * 8];
+  // signed sub-block scales: entry 128 (ls >> 1) + i holds the f16 pairs
+  // (+-ls, +-ls) of sign index i, so (g * ls) with its sign is one multiply
+  __shared__ u32x4 s_lsign[16 * 128];
   __shared__ uint32_t s_pair[kGuBM], s_xrow[kGuBM], s_qrow[kGuBM];
 
   const TileSlab ts = xcd_tile_slab((int)a.tile_offsets[a.E], a.I / kGuBN);
@@ -223,18 +223,20 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
   }
   load_iq2_half_tables(&tab);
   __syncthreads();
-  for (int i = tid; i < 256 * 16; i += kGuThreads) {
-    const uint4 g = tab.gridh[i >> 4];
-    s_grid16[i] = u32x4{g.x, g.y, g.z, g.w};
+  for (int i = tid; i < 256 * 8; i += kGuThreads) {
+    const uint4 g = tab.gridh[i >> 3];
+    s_grid8[i] = u32x4{g.x, g.y, g.z, g.w};
+  }
+  for (int i = tid; i < 16 * 128; i += kGuThreads) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const uint4 sg = tab.sign[i & 127];
+    const _Float16 l = (_Float16)(float)(2 * (i >> 7) + 1);
+    const h2 lp = {l, l};
+    auto m = [&](uint32_t sv) { return __builtin_bit_cast(uint32_t, lp) ^ sv; };
+    s_lsign[i] = u32x4{m(sg.x), m(sg.y), m(sg.z), m(sg.w)};
   }
   __syncthreads();
-  for (int i = tid; i < 128 * 8; i += kGuThreads) {
-    const uint4 g = tab.sign[i >> 3];
-    s_sign8[i] = u32x4{g.x, g.y, g.z, g.w};
-  }
-  __syncthreads();
-  const u32x4* grid16 = &s_grid16[lane & 15];
-  const u32x4* sign8 = &s_sign8[lane & 7];
+  const u32x4* grid8 = &s_grid8[lane & 7];
 
   // A: wave w's loads per superblock fill slots (kAj w + j) * 64 + lane
   constexpr int kAj = 2048 / 64 / (kGuThreads / 64);
@@ -283,7 +285,6 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
     float16v ag0, ag1, au0, au1;
 #pragma unroll
     for (int i = 0; i < 16; i++) { ag0[i] = 0.0f; ag1[i] = 0.0f; au0[i] = 0.0f; au1[i] = 0.0f; }
-    _Float16 lsg = 1, lsu = 1;
     uint32_t g1 = 0, u1 = 0;
     const u32x4* sa = &sA[buf][0];
 #pragma unroll
@@ -292,18 +293,20 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
       if ((ks & 1) == 0) {
         g1 = qs(gr, 2 * sb + 1);
         u1 = qs(ur, 2 * sb + 1);
-        lsg = (_Float16)(float)(2 * (g1 >> 28) + 1);
-        lsu = (_Float16)(float)(2 * (u1 >> 28) + 1);
       }
       const uint32_t sh0 = 16 * (ks & 1) + 8 * kh, sh1 = 14 * (ks & 1) + 7 * kh;
-      const uint32_t gg = __builtin_amdgcn_ubfe(qs(gr, 2 * sb), sh0, 8), gs = __builtin_amdgcn_ubfe(g1, sh1, 7);
-      const uint32_t ug = __builtin_amdgcn_ubfe(qs(ur, 2 * sb), sh0, 8), us = __builtin_amdgcn_ubfe(u1, sh1, 7);
-      const u32x4 gv = grid16[16 * gg], uv = grid16[16 * ug];
-      const u32x4 gsv = sign8[8 * gs], usv = sign8[8 * us];
-      const half8 bg = __builtin_bit_cast(half8, iq2_half8(make_uint4(gv.x, gv.y, gv.z, gv.w),
-                                                           make_uint4(gsv.x, gsv.y, gsv.z, gsv.w), lsg));
-      const half8 bu = __builtin_bit_cast(half8, iq2_half8(make_uint4(uv.x, uv.y, uv.z, uv.w),
-                                                           make_uint4(usv.x, usv.y, usv.z, usv.w), lsu));
+      const uint32_t gg = __builtin_amdgcn_ubfe(qs(gr, 2 * sb), sh0, 8);
+      const uint32_t ug = __builtin_amdgcn_ubfe(qs(ur, 2 * sb), sh0, 8);
+      // sign index (7 bits) and the scale code (top 4 bits) of the sub-block
+      const uint32_t gs = __builtin_amdgcn_ubfe(g1, sh1, 7) | ((g1 >> 28) << 7);
+      const uint32_t us = __builtin_amdgcn_ubfe(u1, sh1, 7) | ((u1 >> 28) << 7);
+      const u32x4 gv = grid8[8 * gg], uv = grid8[8 * ug], gm = s_lsign[gs], um = s_lsign[us];
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      auto mul = [](uint32_t x, uint32_t y) {
+        return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, x) * __builtin_bit_cast(h2, y));
+      };
+      const half8 bg = __builtin_bit_cast(half8, u32x4{mul(gv.x, gm.x), mul(gv.y, gm.y), mul(gv.z, gm.z), mul(gv.w, gm.w)});
+      const half8 bu = __builtin_bit_cast(half8, u32x4{mul(uv.x, um.x), mul(uv.y, um.y), mul(uv.z, um.z), mul(uv.w, um.w)});
       const int c = (2 * ks + kh) ^ l32;
       const half8 a0 = __builtin_bit_cast(half8, sa[l32 * 32 + c]);
       const half8 a1 = __builtin_bit_cast(half8, sa[(32 + l32) * 32 + c]);
