@@ -557,6 +557,20 @@ def test_layer_c5_zipf_sampled(gpu):
     assert top10 > 0.5
 
 
+def test_layer_many_experts_batch_on_the_row_path(gpu):
+    """n_expert above the dispatch limit (576 > 512, 9 groups of 64): a
+    context for 12 tokens has no grouped buffers, so the batch runs the
+    row-streaming launches with T > 8 (no in-launch counters, selection in
+    every routed workgroup); routing and outputs against the oracle, twice
+    on the same context."""
+    import dataclasses
+    base = C.CASES["c1"]
+    cfg = dataclasses.replace(base.cfg, d_model=1024, d_ff=512, n_expert=576, top_k=6, n_group=9, topk_group=4,
+                              d_ff_shared=512)
+    case = dataclasses.replace(base, name="e576", cfg=cfg, T=12, d_ff_real=512, d_ff_shared_real=512)
+    _run_layer(case, 12, gpu)
+
+
 @pytest.mark.parametrize("name,Ts", [("c1", [1, 3, 8, 5]), ("c2", [1, 2, 8])])
 def test_decode_calls_in_a_row(gpu, name, Ts):
     """One context, decode calls of varying T in a row: every call matches the
