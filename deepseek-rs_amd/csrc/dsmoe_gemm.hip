@@ -824,6 +824,196 @@ DSM_Q80_KERNEL(dsmoe_q80_gemm_j2, false, 2)
 #undef DSM_Q80_KERNEL
 
 // ---------------------------------------------------------------------------
+// Shared expert for large batches: the same products as dsmoe_q80_gemm
+// (matmul_q8_0_preq_batch_warp8, matmul.rs:412-458), with the blocks added
+// in order 0, 1, 2, ... instead of the reference's 32-lane tree.
+//
+// dsmoe_q80_unpack rewrites each Q8_0 matrix once per call into the wide
+// GEMM's operand layout (Q80UnpackArgs): 34-byte blocks do not allow aligned
+// operand loads, the rewritten codes are one 16-byte load per lane and
+// block.  Workgroup = 16 rows x 16 blocks: the rows' bytes are read whole
+// into LDS, then written out as f16 codes (exact) and f32 scales.
+// grid = (rows / 16 * ceil(nb / 16), matrices), 256 threads.
+// ---------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(256) void dsmoe_q80_unpack(const Q80UnpackArgs a) {
+  __shared__ uint32_t raw[16][136];  // 16 rows x 16 blocks x 34 bytes
+  const int m = blockIdx.y, nb = a.nb[m], nbt = (nb + 15) >> 4;
+  const int R = blockIdx.x / nbt, b0 = (blockIdx.x % nbt) * 16;
+  if (R >= a.rows[m] / 16) return;
+  const int nbc = min(16, nb - b0), dw = nbc * 17 / 2;  // nb is even: whole dwords
+  const int tid = threadIdx.x;
+  for (int i = tid; i < 16 * dw; i += 256) {
+    const int r = i / dw, k = i - r * dw;
+    raw[r][k] = *(const uint32_t*)(a.w[m] + ((size_t)(16 * R + r) * nb + b0) * Q8_0_BYTES + 4 * k);
+  }
+  __syncthreads();
+  const uint8_t* rb = (const uint8_t*)&raw[0][0];
+  for (int i = tid; i < nbc * 64; i += 256) {
+    const int bb = i >> 6, l = i & 63, r = l & 15, q = l >> 4;
+    const uint8_t* blk = rb + r * 544 + bb * Q8_0_BYTES;
+    uint32_t h[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      const h2 v = {(_Float16)(float)(int8_t)blk[2 + 8 * q + 2 * j], (_Float16)(float)(int8_t)blk[3 + 8 * q + 2 * j]};
+      h[j] = __builtin_bit_cast(uint32_t, v);
+    }
+    const size_t u = (size_t)R * nb + b0 + bb;
+    *(u32x4*)(a.wh[m] + (u * 64 + l) * 8) = u32x4{h[0], h[1], h[2], h[3]};
+    if (q == 0) a.ws[m][u * 16 + r] = f16_to_f32_ftz((uint16_t)(blk[0] | (blk[1] << 8)));
+  }
+}
+
+// dsmoe_q80_wide[_swiglu]: kQwWaves = 8 waves x kQwBT = 256 tokens x
+// kQwRows = 128 rows (kQwRowsSw = 64 rows of gate and the same rows of up).
+// Wave w = 2 rw + th takes tokens 128 th .. +127 of the tile and rows
+// 32 rw .. +31 (16 rw .. +15 of gate and of up): 8 x 2 tiles of 16 x 16.
+// Per Q8_0 block, one v_mfma_f32_16x16x32_f16 per tile gives the block's
+// integer sum (|sum| < 2^19, exact); its value (d_w * d_x) * sum is added to
+// the running sum with one fma.
+// A (token codes, shared by the 8 waves): 2 blocks x 256 tokens per LDS
+// stage, two stages, loaded straight into LDS; chunk q of token t at slot
+// 4 t + (q ^ ((t >> 2) & 3)), so the reads of 16 tokens x 4 chunks are
+// conflict-free.  The token scales per block in token order (a lane's four
+// output tokens are one 16-byte read).
+// B (weights): lane l holds row l % 16 of the tile, codes 8 (l / 16) .. +7,
+// one 16-byte load from the unpacked matrix one stage ahead, and the row's
+// block scale (one dword): the output column of lane l is that row.
+// grid = 8 * ceil(ceil(T / 256) / 8) * out_dim / rows (xcd_slab_tile).
+// ---------------------------------------------------------------------------
+namespace {
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <bool kSw, int NW>
+__device__ __forceinline__ void q80_wide(const Q80WideArgs& a) {
+  constexpr int SB = 2;            // blocks per stage
+  constexpr int BT = 64 * NW / 2;  // tokens per workgroup (128 per wave)
+  __shared__ __align__(16) u32x4 sX[2][SB][4 * BT];
+  __shared__ __align__(16) float sS[2][SB][BT];
+  constexpr int kRows = (kSw ? 16 : 32) * (NW / 2);
+  constexpr int NTH = 64 * NW;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int th = w & 1, rw = w >> 1;
+  const int T = a.T, in = a.in_dim, nb = in >> 5, nst = nb / SB;
+  const TileSlab ts = xcd_slab_tile((T + BT - 1) / BT, a.out_dim / kRows);
+  if (!ts.ok) return;
+  const int m0 = ts.t * BT, n0 = ts.n * kRows;
+  const int c = lane & 15, q = lane >> 4;
+
+  // token codes: slots tid + NTH h of each block's 4 BT
+  constexpr int XH = 4 * BT / NTH;
+  const int tl = tid >> 2, tq = (tid & 3) ^ ((tl >> 2) & 3);
+  const uint8_t* xsrc[XH];
+#pragma unroll
+  for (int h = 0; h < XH; h++)
+    xsrc[h] = (const uint8_t*)(a.xh + (size_t)min(m0 + tl + NTH / 4 * h, T - 1) * in) + 16 * tq;
+  // token scales: slot tid < SB * BT = block tid / BT, token tid % BT
+  const float* ssrc = a.xs + (size_t)min(m0 + tid % BT, T - 1) * nb + tid / BT;
+  auto issue_x = [&](int st, int buf) {
+#pragma unroll
+    for (int j = 0; j < SB; j++)
+#pragma unroll
+      for (int h = 0; h < XH; h++)
+        __builtin_amdgcn_global_load_lds((glb_void*)(xsrc[h] + 64 * (size_t)(st * SB + j)),
+                                         (lds_void*)&sX[buf][j][64 * w + NTH * h], 16, 0, 0);
+    if (64 * w < SB * BT)
+      __builtin_amdgcn_global_load_lds((glb_void*)(ssrc + st * SB), (lds_void*)(&sS[buf][0][0] + 64 * w), 4, 0, 0);
+  };
+  // weight tiles of this wave (nt = 0, 1): 16-row tile index
+  const int R0 = kSw ? n0 / 16 + rw : n0 / 16 + 2 * rw, R1 = kSw ? R0 : R0 + 1;
+  const uint16_t* wh0 = a.w0h + ((size_t)R0 * nb * 64 + lane) * 8;
+  const uint16_t* wh1 = (kSw ? a.w1h : a.w0h) + ((size_t)R1 * nb * 64 + lane) * 8;
+  const float* ws0 = a.w0s + (size_t)R0 * nb * 16 + c;
+  const float* ws1 = (kSw ? a.w1s : a.w0s) + (size_t)R1 * nb * 16 + c;
+  u32x4 wc[2][SB][2];
+  float wv[2][SB][2];
+  auto load_w = [&](int st, auto buf_tag) {
+    constexpr int buf = decltype(buf_tag)::value;
+#pragma unroll
+    for (int j = 0; j < SB; j++) {
+      const size_t b = (size_t)(st * SB + j);
+      wc[buf][j][0] = *(const u32x4*)(wh0 + b * 512);
+      wc[buf][j][1] = *(const u32x4*)(wh1 + b * 512);
+      wv[buf][j][0] = ws0[b * 16];
+      wv[buf][j][1] = ws1[b * 16];
+    }
+  };
+
+  f32x4 run[8][2];
+#pragma unroll
+  for (int mt = 0; mt < 8; mt++)
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) run[mt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](auto buf_tag) {
+    constexpr int buf = decltype(buf_tag)::value;
+#pragma unroll
+    for (int j = 0; j < SB; j++) {
+      const half8 b0 = __builtin_bit_cast(half8, wc[buf][j][0]), b1 = __builtin_bit_cast(half8, wc[buf][j][1]);
+#pragma unroll
+      for (int mt = 0; mt < 8; mt++) {
+        const int t = 128 * th + 16 * mt + c;
+        const half8 ax = __builtin_bit_cast(half8, sX[buf][j][4 * t + (q ^ ((t >> 2) & 3))]);
+        const f32x4 sx = *(const f32x4*)&sS[buf][j][128 * th + 16 * mt + 4 * q];
+        const f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, b0, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        const f32x4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, b1, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          run[mt][0][i] = __builtin_fmaf(wv[buf][j][0] * sx[i], s0[i], run[mt][0][i]);
+          run[mt][1][i] = __builtin_fmaf(wv[buf][j][1] * sx[i], s1[i], run[mt][1][i]);
+        }
+      }
+    }
+  };
+
+  issue_x(0, 0);
+  load_w(0, std::integral_constant<int, 0>{});
+  for (int st = 0; st < nst; st += 2) {  // an odd stage count ends at the break
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (st + 1 < nst) {
+      issue_x(st + 1, 1);
+      load_w(st + 1, std::integral_constant<int, 1>{});
+    }
+    compute(std::integral_constant<int, 0>{});
+    if (st + 1 >= nst) break;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (st + 2 < nst) {
+      issue_x(st + 2, 0);
+      load_w(st + 2, std::integral_constant<int, 0>{});
+    }
+    compute(std::integral_constant<int, 1>{});
+  }
+
+  // lane l: column (row of the weights) l % 16 of each tile, tokens 4 q .. +3 of each token tile
+#pragma unroll
+  for (int mt = 0; mt < 8; mt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int tok = m0 + 128 * th + 16 * mt + 4 * q + i;
+      if (tok >= T) continue;
+      float* o = a.out + (size_t)tok * a.out_dim;
+      if (kSw) {
+        const float g = clamp_gate(run[mt][0][i], a.clamp), u = clamp_up(run[mt][1][i], a.clamp);
+        o[n0 + 16 * rw + c] = (g / (1.0f + expf_dsm(-g))) * u * 1.0f;
+      } else {
+        o[n0 + 32 * rw + c] = run[mt][0][i];
+        o[n0 + 32 * rw + 16 + c] = run[mt][1][i];
+      }
+    }
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(64 * kQwWaves) void dsmoe_q80_wide(const Q80WideArgs a) {
+  q80_wide<false, kQwWaves>(a);
+}
+extern "C" __global__ __launch_bounds__(64 * kQwWaves) void dsmoe_q80_wide_swiglu(const Q80WideArgs a) {
+  q80_wide<true, kQwWaves>(a);
+}
+
+// ---------------------------------------------------------------------------
 // Router logits for batches (matmul_f16, matmul.rs:57-105): workgroup =
 // 8 experts x 16 tokens.  For each (token, expert) thread tx sums elements
 // tx, tx+256, ... in order (f32 multiply, then add), and the halving tree

@@ -84,7 +84,8 @@ const std::vector<uint8_t>& lvlmap_host() {
 enum Kern { K_PREP, K_ROUTER_SELECT, K_UP, K_MIDQ, K_DN, K_SWIGLU, K_MOE_SUM, K_DISPATCH, K_SYNTH,
             K_GU_GROUPED, K_DN_GROUPED, K_Q80_GEMM_SWIGLU, K_Q80_GEMM,
             K_ROUTER_TILE, K_UP_ROWS, K_DN_ROWS, K_Q80_GEMM_SWIGLU_J7, K_Q80_GEMM_J7, K_Q80_GEMM_SWIGLU_J2,
-            K_Q80_GEMM_J2, K_HC_EXPAND, K_PROBE_MFMA, K_PROBE_READ, K_UP_EM, K_DN_EM, K_Q80_COMBINE, K_SELECT_HASH, K_RMS_NORM, K_HC_SPLIT_NORM, K_COUNT };
+            K_Q80_GEMM_J2, K_HC_EXPAND, K_PROBE_MFMA, K_PROBE_READ, K_UP_EM, K_DN_EM, K_Q80_COMBINE, K_SELECT_HASH, K_RMS_NORM, K_HC_SPLIT_NORM,
+            K_Q80_UNPACK, K_Q80_WIDE, K_Q80_WIDE_SW, K_COUNT };
 const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_up", "dsmoe_midq", "dsmoe_dn",
                                    "dsmoe_swiglu", "dsmoe_moe_sum", "dsmoe_dispatch", "dsmoe_synth",
                                    "dsmoe_gu_grouped", "dsmoe_dn_grouped", "dsmoe_q80_gemm_swiglu", "dsmoe_q80_gemm",
@@ -93,9 +94,11 @@ const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_u
                                    "dsmoe_q80_gemm_swiglu_j2", "dsmoe_q80_gemm_j2", "dsmoe_hc_expand",
                                    "dsmoe_probe_mfma", "dsmoe_probe_read", "dsmoe_up_em", "dsmoe_dn_em",
                                    "dsmoe_q80_combine", "dsmoe_router_select_hash",
-                                   "dsmoe_rms_norm_plain", "dsmoe_hc_split_norm"};
+                                   "dsmoe_rms_norm_plain", "dsmoe_hc_split_norm", "dsmoe_q80_unpack", "dsmoe_q80_wide",
+                                   "dsmoe_q80_wide_swiglu"};
 // code object of each kernel: 0 = dsmoe_kernels.hsaco, 1 = dsmoe_gemm.hsaco (same directory)
-const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0, 1, 1, 0, 0, 1, 0, 0, 0};
+const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0, 1, 1, 0, 0, 1, 0, 0, 0,
+                                  1, 1, 1};
 static_assert(DSMOE_GROUPED_TILE_M == kGuBM, "header and kernels disagree on the grouped tile");
 
 extern "C" int dsmoe_noalloc_setup(void** ptr, size_t* bytes);  // dsmoe_noalloc.hip
@@ -737,6 +740,74 @@ int dsmoe_q8_0_gemm(const void* w0, const void* w1, const uint16_t* xh, const fl
   return q80_gemm_impl(w0, w1, xh, xscale, out, in_dim, out_dim, T, clamp, nullptr, 1, stream);
 }
 
+// Shared expert for large batches: the Q8_0 matrices rewritten into the wide
+// GEMM's operand layout once per call, then dsmoe_q80_wide[_swiglu] (blocks
+// added in order; the exact kernels above keep the reference's tree).
+// Batches of at least q80_wide_min_t() tokens take it: below that the grid of
+// 128-token tiles is too small to fill the chip and the split exact kernel
+// is faster.
+static int q80_wide_min_t() { return DSM_TUNE("DSM_Q80_WIDE_MIN_T", 1024); }
+static bool q80_wide_fits(int d, int Is) {
+  return d % 128 == 0 && Is % 64 == 0 && d <= 8192 && Is <= 8192;
+}
+static int q80_unpack(const void* const* w, uint16_t* const* wh, float* const* ws, const int* rows, const int* nb, int n,
+                      dsmoe_stream_t stream) {
+  Q80UnpackArgs a{};
+  unsigned units = 0;
+  for (int m = 0; m < n; m++) {
+    if (rows[m] % 16 || nb[m] % 2 || !aligned16(wh[m]) || (size_t)w[m] % 4)
+      return fail(DSMOE_ERR_UNSUPPORTED, "q80_unpack: shape or alignment outside what the kernel assumes");
+    a.w[m] = (const uint8_t*)w[m];
+    a.wh[m] = wh[m];
+    a.ws[m] = ws[m];
+    a.rows[m] = rows[m];
+    a.nb[m] = nb[m];
+    units = std::max(units, (unsigned)(rows[m] / 16 * ((nb[m] + 15) / 16)));
+  }
+  return launch(K_Q80_UNPACK, dim3(units, (unsigned)n), dim3(256), 0, stream, a);
+}
+static int q80_wide_impl(const uint16_t* w0h, const float* w0s, const uint16_t* w1h, const float* w1s,
+                         const uint16_t* xh, const float* xs, float* out, int in_dim, int out_dim, int T, float clamp,
+                         dsmoe_stream_t stream) {
+  const int rows = w1h ? kQwRowsSw : kQwRows;
+  if (in_dim % 64 || out_dim % rows || T <= 0 || !aligned16(xh) || !aligned16(out))
+    return fail(DSMOE_ERR_UNSUPPORTED, "q80_wide: shape or alignment outside what the kernel assumes");
+  Q80WideArgs a{w0h, w0s, w1h, w1s, xh, xs, out, in_dim, out_dim, T, clamp};
+  return launch(w1h ? K_Q80_WIDE_SW : K_Q80_WIDE, dim3(xcd_grid((T + kQwBT - 1) / kQwBT, out_dim / rows)),
+                dim3(64 * kQwWaves), 0, stream, a);
+}
+
+extern "C" {
+
+int dsmoe_q8_0_unpack(const void* w, int32_t rows, int32_t in_dim, uint16_t* codes, float* scales,
+                      dsmoe_stream_t stream) {
+  if (!w || !codes || !scales) return fail(DSMOE_ERR_INVALID, "q8_0_unpack: null pointer");
+  if (rows <= 0 || rows % 16 || in_dim <= 0 || in_dim % 64)
+    return fail(DSMOE_ERR_UNSUPPORTED, "q8_0_unpack: rows a multiple of 16, in_dim of 64");
+  if (!aligned16(codes) || (uintptr_t)w % 4) return fail(DSMOE_ERR_INVALID, "q8_0_unpack: codes 16-byte, w 4-byte aligned");
+  const void* ws[1] = {w};
+  uint16_t* hs[1] = {codes};
+  float* ss[1] = {scales};
+  const int r[1] = {rows}, nb[1] = {in_dim / 32};
+  return q80_unpack(ws, hs, ss, r, nb, 1, stream);
+}
+
+int dsmoe_q8_0_gemm_unpacked(const uint16_t* w0h, const float* w0s, const uint16_t* w1h, const float* w1s,
+                             const uint16_t* xh, const float* xscale, float* out, int32_t in_dim, int32_t out_dim,
+                             int32_t T, float clamp, dsmoe_stream_t stream) {
+  if (!w0h || !w0s || !xh || !xscale || !out || (!w1h) != (!w1s))
+    return fail(DSMOE_ERR_INVALID, "q8_0_gemm_unpacked: null pointer");
+  if (!aligned16(w0h) || (w1h && !aligned16(w1h)) || !aligned16(xh) || !aligned16(out))
+    return fail(DSMOE_ERR_INVALID, "q8_0_gemm_unpacked: codes, xh and out must be 16-byte aligned");
+  if (in_dim <= 0 || in_dim % 64 || in_dim > 8192 || T < 0 || out_dim <= 0 || out_dim % (w1h ? kQwRowsSw : kQwRows))
+    return fail(DSMOE_ERR_UNSUPPORTED,
+                "q8_0_gemm_unpacked: in_dim a multiple of 64 (<= 8192), out_dim of 64 (two matrices) or 128");
+  if (T == 0) return DSMOE_OK;
+  return q80_wide_impl(w0h, w0s, w1h, w1s, xh, xscale, out, in_dim, out_dim, T, clamp, stream);
+}
+
+}  // extern "C"
+
 // --------------------------------------------------------------------------
 // Context + whole layer
 // --------------------------------------------------------------------------
@@ -773,6 +844,8 @@ struct dsmoe_ctx {
   uint32_t* g_tile_experts = nullptr;
   uint32_t* g_tile_starts = nullptr;
   float* q80_part = nullptr;     // split shared-expert GEMM partials, [kQ80MaxSplit][min(T, 256)][cols]
+  uint16_t* shw_h[3] = {};       // shared gate / up / down unpacked for dsmoe_q80_wide (codes as f16)
+  float* shw_s[3] = {};          // their block scales
   // hash routing (dsmoe_set_hash_routing): table [hash_rows][k], token ids [T]
   const int32_t* hash = nullptr;
   const int32_t* hash_tokens = nullptr;
@@ -949,6 +1022,13 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
     A(&c->g_tile_experts, max_tiles * 4);
     A(&c->g_tile_starts, max_tiles * 4);
     A(&c->q80_part, (size_t)kQ80MaxSplit * std::min<size_t>(T, 256) * std::max<size_t>(2 * Is, d) * 4);
+    if (cfg->shared_fmt == 0 && q80_wide_fits((int)d, cfg->d_ff_shared) && max_tokens >= q80_wide_min_t()) {
+      const size_t is = (size_t)cfg->d_ff_shared;
+      for (int m = 0; m < 3; m++) {
+        A(&c->shw_h[m], is * d * 2);
+        A(&c->shw_s[m], is * d / 32 * 4);
+      }
+    }
   }
   if (rc != DSMOE_OK) {
     std::string msg = g_err;
@@ -996,6 +1076,8 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // stream their weights once per chunk of em_pairs() pairs
   // (expert-major matvec) instead of dequantizing them into MFMA tiles.
   const bool em = grouped && (int64_t)P <= (int64_t)kEmMaxLoad * E && em_fits(cf);
+  // Large batches run the shared expert through the unpacked wide GEMM.
+  const bool wide = grouped && cf.shared_fmt == 0 && c->shw_h[0] != nullptr && T >= q80_wide_min_t();
   // In the row-streaming path the selection needs no launch of its own:
   // every routed gate/up workgroup runs it for its token.
   const bool up_rows = !grouped && up_rows_fits(d) && (cf.shared_fmt != 0 || q80_rows_fits(d));
@@ -1071,8 +1153,16 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     if (grouped && cf.shared_fmt == 0) {  // shared expert as a GEMM over the whole batch
       a.sh_work = 0;
       StageScope sg(c, DSMOE_STAGE_SH_UP, stream);
-      DSM_TRY(q80_gemm_impl(w->sh_gate, w->sh_up, c->xh80, c->xs80, c->sh_mid, d, Is, T, cf.swiglu_clamp,
-                            T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, stream));
+      if (wide) {
+        const void* ws[2] = {w->sh_gate, w->sh_up};
+        const int rows[2] = {Is, Is}, nbs[2] = {d / 32, d / 32};
+        DSM_TRY(q80_unpack(ws, c->shw_h, c->shw_s, rows, nbs, 2, stream));
+        DSM_TRY(q80_wide_impl(c->shw_h[0], c->shw_s[0], c->shw_h[1], c->shw_s[1], c->xh80, c->xs80, c->sh_mid, d, Is,
+                              T, cf.swiglu_clamp, stream));
+      } else {
+        DSM_TRY(q80_gemm_impl(w->sh_gate, w->sh_up, c->xh80, c->xs80, c->sh_mid, d, Is, T, cf.swiglu_clamp,
+                              T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, stream));
+      }
     }
     if (fuse_midq) {
       a.fuse_midq = 1;
@@ -1129,8 +1219,16 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     if (grouped && cf.shared_fmt == 0) {
       a.sh_work = 0;
       StageScope sg(c, DSMOE_STAGE_SH_DN, stream);
-      DSM_TRY(q80_gemm_impl(w->sh_down, nullptr, c->shh, c->sh_s80, shared_out, Is, d, T, 0.0f,
-                            T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, stream));
+      if (wide) {
+        const void* ws[1] = {w->sh_down};
+        const int rows[1] = {d}, nbs[1] = {Is / 32};
+        DSM_TRY(q80_unpack(ws, c->shw_h + 2, c->shw_s + 2, rows, nbs, 1, stream));
+        DSM_TRY(q80_wide_impl(c->shw_h[2], c->shw_s[2], nullptr, nullptr, c->shh, c->sh_s80, shared_out, Is, d, T,
+                              0.0f, stream));
+      } else {
+        DSM_TRY(q80_gemm_impl(w->sh_down, nullptr, c->shh, c->sh_s80, shared_out, Is, d, T, 0.0f,
+                              T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, stream));
+      }
     }
     if (rows) {
       a.dn_tiles = (d + kDnRowsR - 1) / kDnRowsR;

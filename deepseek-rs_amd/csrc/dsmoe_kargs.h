@@ -251,6 +251,38 @@ struct Q80CombineArgs {
   float clamp;
 };
 
+// Shared expert for large batches, step 1: Q8_0 matrices rewritten in the
+// operand layout of the wide GEMM (dsmoe_q80_unpack).  Row tile R (16 rows)
+// and block b: codes at wh[((R * nb + b) * 64 + l) * 8 ..+8] as f16 for lane
+// l = 16 q + r (row 16 R + r, codes 8 q .. 8 q + 7 of the block), and the 16
+// rows' block scales as f32 at ws[(R * nb + b) * 16 ..+16].  Up to three
+// matrices per launch (grid.y).
+struct Q80UnpackArgs {
+  const uint8_t* w[3];  // Q8_0 [rows][nb]
+  uint16_t* wh[3];
+  float* ws[3];
+  int32_t rows[3], nb[3];
+};
+
+// Step 2: dsmoe_q80_wide / dsmoe_q80_wide_swiglu over the unpacked weights.
+// Workgroup = kQwWaves waves x kQwBT tokens x kQwRows rows (kQwRowsSw row
+// pairs of gate and up with SwiGLU).
+struct Q80WideArgs {
+  const uint16_t* w0h;  // unpacked gate (or the single matrix)
+  const float* w0s;
+  const uint16_t* w1h;  // unpacked up, or null
+  const float* w1s;
+  const uint16_t* xh;   // activation codes as f16 [T][in_dim]
+  const float* xs;      // activation block scales [T][in_dim/32]
+  float* out;           // [T][out_dim]
+  int32_t in_dim, out_dim, T;
+  float clamp;
+};
+#ifndef DSM_QW_WAVES
+#define DSM_QW_WAVES 8
+#endif
+enum { kQwWaves = DSM_QW_WAVES, kQwBT = 32 * kQwWaves, kQwRows = 16 * kQwWaves, kQwRowsSw = 8 * kQwWaves };
+
 struct SwigluArgs {
   const float* gate;
   const float* up;

@@ -30,7 +30,7 @@ EXPORTED = [
     "dsmoe_q8_0_matvec", "dsmoe_swiglu", "dsmoe_dispatch", "dsmoe_tensor_bytes", "dsmoe_synth_tensor",
     "dsmoe_synth_tensor_host", "dsmoe_stage_name", "dsmoe_set_profiling", "dsmoe_profile_read",
     "dsmoe_q8k_quantize_h", "dsmoe_gate_up_mid_sorted", "dsmoe_down_sorted", "dsmoe_q8_0_quantize_h",
-    "dsmoe_q8_0_gemm",
+    "dsmoe_q8_0_gemm", "dsmoe_q8_0_unpack", "dsmoe_q8_0_gemm_unpacked",
     "dsmoe_gguf_open", "dsmoe_gguf_close", "dsmoe_gguf_tensor_count", "dsmoe_gguf_data_offset", "dsmoe_gguf_tensor_at",
     "dsmoe_gguf_find", "dsmoe_gguf_kv_u32", "dsmoe_gguf_kv_i32_array", "dsmoe_gguf_moe_layer",
     "dsmoe_router_select_hash", "dsmoe_set_hash_routing", "dsmoe_rms_norm_plain", "dsmoe_hc_split_norm",
@@ -95,6 +95,8 @@ def lib():
         "dsmoe_down_sorted": ([vp] * 9 + [i32] * 4 + [vp], i32),
         "dsmoe_q8_0_quantize_h": ([vp, vp, vp, vp, i32, i32, vp], i32),
         "dsmoe_q8_0_gemm": ([vp, vp, vp, vp, vp, i32, i32, i32, f32, vp], i32),
+        "dsmoe_q8_0_unpack": ([vp, i32, i32, vp, vp, vp], i32),
+        "dsmoe_q8_0_gemm_unpacked": ([vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, f32, vp], i32),
         "dsmoe_gate_up_mid": ([vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, vp], i32),
         "dsmoe_down": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp], i32),
         "dsmoe_moe_sum": ([vp, vp, i32, i32, i32, vp], i32),
@@ -250,6 +252,19 @@ def q8_0_quantize_h(x, xq, xscale, out_h, in_dim, rows, stream=None):
 def q8_0_gemm(w0, w1, xh, xscale, out, in_dim, out_dim, T, clamp=0.0, stream=None):
     check(lib().dsmoe_q8_0_gemm(_p(w0), _p(w1), _p(xh), _p(xscale), _p(out), in_dim, out_dim, T, clamp,
                                 _stream(stream)))
+
+
+def q8_0_unpack(w, rows, in_dim, codes, scales, stream=None):
+    """A Q8_0 matrix rewritten for q8_0_gemm_unpacked: codes f16 [rows * in_dim],
+    scales f32 [rows * in_dim / 32]."""
+    check(lib().dsmoe_q8_0_unpack(_p(w), rows, in_dim, _p(codes), _p(scales), _stream(stream)))
+
+
+def q8_0_gemm_unpacked(w0h, w0s, w1h, w1s, xh, xscale, out, in_dim, out_dim, T, clamp=0.0, stream=None):
+    """q8_0_gemm over unpacked matrices, blocks added in order (f32 rounding
+    of the reference's sum order)."""
+    check(lib().dsmoe_q8_0_gemm_unpacked(_p(w0h), _p(w0s), _p(w1h), _p(w1s), _p(xh), _p(xscale), _p(out), in_dim,
+                                         out_dim, T, clamp, _stream(stream)))
 
 
 def q8_0_quantize(x, xq, xscale, in_dim, rows, stream=None):

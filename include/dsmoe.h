@@ -321,6 +321,27 @@ int dsmoe_q8_0_matvec(const void* w, const int8_t* xq, const float* xscale, floa
 int dsmoe_q8_0_gemm(const void* w0, const void* w1, const uint16_t* xh, const float* xscale, float* out, int32_t in_dim,
                     int32_t out_dim, int32_t T, float clamp, dsmoe_stream_t stream);
 
+/* The shared-expert GEMM for large batches, no reference counterpart in
+ * form (the products of matmul_q8_0_preq_batch_warp8, matmul.rs:412-458).
+ * dsmoe_q8_0_unpack rewrites a Q8_0 matrix [rows][in_dim/32 blocks] into
+ * the operand layout of dsmoe_q8_0_gemm_unpacked: codes as f16
+ * (rows * in_dim of them) and block scales as f32 (rows * in_dim / 32); an
+ * engine can do this once per weight load.  rows a multiple of 16, in_dim of
+ * 64; codes 16-byte and w 4-byte aligned.
+ * dsmoe_q8_0_gemm_unpacked is dsmoe_q8_0_gemm over unpacked matrices (w1h /
+ * w1s NULL for one matrix) with each block's value (d_w * d_x) * sum added
+ * to the running sum in block order by one fma, where the reference adds
+ * 32 lane-strided partials and then halves them: equal to dsmoe_q8_0_gemm up
+ * to f32 rounding of that order (the integer sums are the same).  in_dim a
+ * multiple of 64, at most 8192; out_dim a multiple of 128 (one matrix) or 64
+ * (two); xh and out 16-byte aligned.  Full speed from about 1024 tokens (a
+ * workgroup takes 256 tokens). */
+int dsmoe_q8_0_unpack(const void* w, int32_t rows, int32_t in_dim, uint16_t* codes, float* scales,
+                      dsmoe_stream_t stream);
+int dsmoe_q8_0_gemm_unpacked(const uint16_t* w0h, const float* w0s, const uint16_t* w1h, const float* w1s,
+                             const uint16_t* xh, const float* xscale, float* out, int32_t in_dim, int32_t out_dim,
+                             int32_t T, float clamp, dsmoe_stream_t stream);
+
 /* swiglu (engine/src/kernels/utils.rs:141-163). */
 int dsmoe_swiglu(const float* gate, const float* up, float* out, int32_t n, float clamp, float weight,
                  dsmoe_stream_t stream);

@@ -398,6 +398,58 @@ def test_q8_0_gemm_matches_matvec(gpu, din, dout, T):
     assert bits_equal(np_(mid), np_(mid_ref))
 
 
+@pytest.mark.parametrize("din,dout,T", [(7168, 2048, 1100), (2048, 7168, 1030), (2048, 1408, 300),
+                                         (4096, 1024, 257), (1408, 2048, 3)])
+def test_q8_0_gemm_unpacked(gpu, din, dout, T):
+    """The unpacked layout against a numpy restatement (same bits), and the
+    unpacked GEMM (blocks added in order) against dsmoe_q8_0_gemm, the
+    reference's sum order, which the matvec test above pins: 1e-5 relative
+    L2 and 1e-4 of the largest magnitude per element."""
+    import torch
+    say(f"q8_0 gemm unpacked din={din} dout={dout} T={T}")
+    nb = din // 32
+    w0 = dsmoe.synth(dsmoe.FMT_Q8_0, 6, 1, 1, dout, din, sigma=0.02, device=gpu)
+    w1 = dsmoe.synth(dsmoe.FMT_Q8_0, 6, 2, 1, dout, din, sigma=0.02, device=gpu)
+    x = dsmoe.synth(dsmoe.FMT_F32, 6, 3, 1, T, din, sigma=1.0, device=gpu)
+    xq = torch.empty(T * din, dtype=torch.int8, device=gpu)
+    xs = torch.empty(T * nb, device=gpu)
+    xh = torch.empty(T, din, dtype=torch.int16, device=gpu)
+    dsmoe.q8_0_quantize_h(x, xq, xs, xh, din, T)
+    hs = [torch.empty(dout * din, dtype=torch.int16, device=gpu) for _ in range(2)]
+    ss = [torch.empty(dout * nb, device=gpu) for _ in range(2)]
+    dsmoe.q8_0_unpack(w0, dout, din, hs[0], ss[0])
+    dsmoe.q8_0_unpack(w1, dout, din, hs[1], ss[1])
+    mid = torch.full((T, dout), float("nan"), device=gpu)
+    mid_ref = torch.full((T, dout), float("nan"), device=gpu)
+    dsmoe.q8_0_gemm_unpacked(hs[0], ss[0], hs[1], ss[1], xh, xs, mid, din, dout, T, 10.0)
+    dsmoe.q8_0_gemm(w0, w1, xh, xs, mid_ref, din, dout, T, 10.0)
+    one = dout % 128 == 0
+    if one:
+        out = torch.full((T, dout), float("nan"), device=gpu)
+        out_ref = torch.full((T, dout), float("nan"), device=gpu)
+        dsmoe.q8_0_gemm_unpacked(hs[0], ss[0], None, None, xh, xs, out, din, dout, T)
+        dsmoe.q8_0_gemm(w0, None, xh, xs, out_ref, din, dout, T)
+    torch.cuda.synchronize()
+    # layout: codes [rows / 16][nb][lane 16 q + r][8] = row 16 R + r, codes 8 q .. +7 of the block
+    raw = np_(w0).reshape(dout, nb, 34)
+    codes = raw[:, :, 2:].copy().view(np.int8).astype(np.float16)
+    want = codes.reshape(dout // 16, 16, nb, 4, 8).transpose(0, 2, 3, 1, 4).reshape(-1)
+    assert bits_equal(np_(hs[0]).view(np.float16), want)
+    sc = raw[:, :, :2].copy().view(np.float16).reshape(dout, nb).astype(np.float32)
+    # the reference's f16 conversion flushes subnormal scales to zero (sign kept)
+    sc = np.where(np.abs(sc) < 2.0 ** -14, np.copysign(np.float32(0.0), sc), sc).astype(np.float32)
+    assert bits_equal(np_(ss[0]), sc.reshape(dout // 16, 16, nb).transpose(0, 2, 1).reshape(-1))
+
+    def close(got, ref, what):
+        r = rel_l2(got, ref)
+        err = float(np.abs(got - ref).max() / np.abs(ref).max())
+        say(f"  {what}: rel_l2={r:.3e} max_err/max={err:.3e}")
+        assert r <= 1e-5 and err <= 1e-4, (what, r, err)
+    close(np_(mid), np_(mid_ref), "swiglu(gate, up)")
+    if one:
+        close(np_(out), np_(out_ref), "one matrix")
+
+
 def test_q8_0_matvec_and_swiglu_bitexact(gpu):
     import torch
     say("q8_0 matvec + swiglu")
@@ -555,6 +607,44 @@ def test_layer_c5_zipf_sampled(gpu):
     top10 = np.sort(counts)[::-1][:10].sum() / counts.sum()
     say(f"  top-10 expert share at T=2048 Zipf: {top10:.3f}")
     assert top10 > 0.5
+
+
+@pytest.mark.parametrize("name,T", [("ref", 1100), ("c1", 1030)])
+def test_layer_shared_expert_wide_gemm(gpu, name, T):
+    """Batches of 1024 tokens and more run the shared expert through the
+    unpacked wide GEMM (blocks added in order, not in the reference's lane
+    tree): the layer's shared output against the oracle on rows of the full
+    256-token tiles and of the partial last one, and the same result on a
+    second call."""
+    import torch
+    case = C.with_tokens(C.CASES[name], T)
+    say(f"shared wide gemm {name} T={T}")
+    w = C.make_weights(case, device=gpu)
+    x = C.make_x(case, T=T, device=gpu)
+    d, k = case.cfg.d_model, case.cfg.top_k
+    layer = dsmoe.MoeLayer(case.cfg, T)
+    so = torch.empty(T, d, device=gpu)
+    ro = torch.empty(T, d, device=gpu)
+    sel = torch.empty(T, k, dtype=torch.int32, device=gpu)
+    wt = torch.empty(T, k, device=gpu)
+    layer.forward(w, x, so, ro, sel, wt)
+    so2 = torch.full((T, d), float("nan"), device=gpu)
+    layer.forward(w, x, so2, ro, sel, wt)
+    torch.cuda.synchronize()
+    layer.close()
+    assert bits_equal(np_(so2), np_(so)), "second call differs"
+    rows = np.array(sorted(set(range(0, T, 37)) | {255, 256, 1023, 1024, T - 1}))
+    so0, _, _, _ = O.moe_forward(case.cfg, _host_weights(w), np_(x)[rows].copy(), len(rows), NT)
+    got = np_(so)[rows]
+    r = rel_l2(got, so0)
+    per_row = np.linalg.norm(got - so0, axis=1) / np.linalg.norm(so0, axis=1)
+    say(f"  shared_out rows={len(rows)} rel_l2={r:.3e} median row {np.median(per_row):.3e} max row {per_row.max():.3e}")
+    # the shared mid is quantized again (Q8_0) before the down matrix: where
+    # f32 rounding moves a block's largest element across a rounding step the
+    # block's codes change, so single rows differ by up to about one
+    # quantization step; the rest agree to f32 rounding
+    assert r <= REL_L2, r
+    assert np.median(per_row) <= 1e-5, np.median(per_row)
 
 
 def test_layer_many_experts_batch_on_the_row_path(gpu):
