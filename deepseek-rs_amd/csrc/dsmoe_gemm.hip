@@ -193,8 +193,10 @@ __device__ __forceinline__ void load17(const uint8_t* p, uint32_t* r) {
 
 extern "C" __global__ __launch_bounds__(kGuThreads)
 void dsmoe_gu_grouped(const GuGroupedArgs a) {
-  __shared__ __align__(16) u32x4 sA[2][kGuBM * 32];
-  __shared__ __align__(16) float s_yd[2][kGuBM];
+  // two stage buffers as separate arrays, so the compiler knows that the
+  // direct loads into one do not alias reads of the other
+  __shared__ __align__(16) u32x4 sA0[kGuBM * 32], sA1[kGuBM * 32];
+  __shared__ __align__(16) float s_yd0[kGuBM], s_yd1[kGuBM];
   __shared__ Iq2HalfTables tab;
   // the f16 grid table in 8 copies, entry g of copy p at 8 g + p (p = lane % 8)
   __shared__ u32x4 s_grid8[256 * 8];
@@ -238,22 +240,29 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
   __syncthreads();
   const u32x4* grid8 = &s_grid8[lane & 7];
 
-  // A: wave w's loads per superblock fill slots (kAj w + j) * 64 + lane
+  // A: wave w's loads per superblock fill slots (kAj w + j) * 64 + lane; the
+  // byte offsets are formed from s_xrow at each issue rather than kept in
+  // registers (at this kernel's register use they would be spilled, and a
+  // spill reload waits for every load in flight)
   constexpr int kAj = 2048 / 64 / (kGuThreads / 64);
-  uint32_t aoff[kAj];
-#pragma unroll
-  for (int j = 0; j < kAj; j++) {
-    const int sl = (kAj * w + j) * 64 + lane, m = sl >> 5, c = (sl & 31) ^ (m & 31);
-    aoff[j] = s_xrow[m] + 16u * (uint32_t)c;
-  }
   const uint32_t qoff = s_qrow[lane];
-  auto issue_a = [&](int b, int buf) {
-    const uint8_t* base = (const uint8_t*)a.xh + 512 * b;
+  // activation codes through a buffer descriptor: the per-lane offsets stay
+  // 32-bit registers and the superblock step is the scalar offset
+  const __amdgpu_buffer_rsrc_t rxh = __builtin_amdgcn_make_buffer_rsrc((void*)a.xh, (short)0, 0x7FFFFFFF, kBufDword3);
+  auto issue_a = [&](int b, auto buf_tag) {
+    constexpr bool B1 = decltype(buf_tag)::value;
+    auto& sA = B1 ? sA1 : sA0;
+    auto& s_yd = B1 ? s_yd1 : s_yd0;
+    int lo = lane;  // opaque copy: the offsets are formed here, not hoisted and spilled
+    asm volatile("" : "+v"(lo));
 #pragma unroll
-    for (int j = 0; j < kAj; j++)
-      __builtin_amdgcn_global_load_lds((glb_void*)(base + aoff[j]), (lds_void*)&sA[buf][(kAj * w + j) * 64], 16, 0, 0);
-    if (w == 0)  // the 64 pairs' block scales: lane l -> s_yd[buf][l]
-      __builtin_amdgcn_global_load_lds((glb_void*)(a.xq + qoff + (size_t)b * Q8K_BYTES), (lds_void*)&s_yd[buf][0], 4,
+    for (int j = 0; j < kAj; j++) {
+      const int sl = (kAj * w + j) * 64 + lo, m = sl >> 5, c = (sl & 31) ^ (m & 31);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rxh, (lds_void*)&sA[(kAj * w + j) * 64], 16,
+                                               s_xrow[m] + 16u * (uint32_t)c, 512 * b, 0, 0);
+    }
+    if (w == 0)  // the 64 pairs' block scales: lane l -> s_yd[l]
+      __builtin_amdgcn_global_load_lds((glb_void*)(a.xq + qoff + (size_t)b * Q8K_BYTES), (lds_void*)&s_yd[0], 4,
                                        0, 0);
   };
   const size_t rb = (size_t)nb * IQ2XXS_BYTES;
@@ -269,8 +278,10 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
 
   // one superblock from LDS buffer buf and raw rows gr / ur (kEven: the qs
   // start 2 bytes into the loaded words)
-  auto superblock = [&](auto even_tag, int buf, uint32_t* gr, uint32_t* ur) {
-    constexpr bool kEven = decltype(even_tag)::value;
+  auto superblock = [&](auto even_tag, uint32_t* gr, uint32_t* ur) {
+    constexpr bool kEven = decltype(even_tag)::value;  // even superblocks use buffer 0
+    auto& sA = kEven ? sA0 : sA1;
+    auto& s_yd = kEven ? s_yd0 : s_yd1;
     // the block scale, then the qs words realigned in place (even superblocks
     // start 2 bytes into the loaded words): qs word j is r[j + 1]
     const uint32_t dg = kEven ? gr[0] & 0xFFFF : gr[0] >> 16, du = kEven ? ur[0] & 0xFFFF : ur[0] >> 16;
@@ -286,7 +297,11 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) { ag0[i] = 0.0f; ag1[i] = 0.0f; au0[i] = 0.0f; au1[i] = 0.0f; }
     uint32_t g1 = 0, u1 = 0;
-    const u32x4* sa = &sA[buf][0];
+    // the lane index through an opaque copy: the 16 operand addresses below
+    // are formed here, per superblock, not hoisted out of the loop and spilled
+    int lz = l32;
+    asm volatile("" : "+v"(lz));
+    const u32x4* sa = &sA[0];
 #pragma unroll
     for (int ks = 0; ks < 16; ks++) {
       const int sb = ks >> 1;
@@ -307,9 +322,9 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
       };
       const half8 bg = __builtin_bit_cast(half8, u32x4{mul(gv.x, gm.x), mul(gv.y, gm.y), mul(gv.z, gm.z), mul(gv.w, gm.w)});
       const half8 bu = __builtin_bit_cast(half8, u32x4{mul(uv.x, um.x), mul(uv.y, um.y), mul(uv.z, um.z), mul(uv.w, um.w)});
-      const int c = (2 * ks + kh) ^ l32;
-      const half8 a0 = __builtin_bit_cast(half8, sa[l32 * 32 + c]);
-      const half8 a1 = __builtin_bit_cast(half8, sa[(32 + l32) * 32 + c]);
+      const int c = (2 * ks + kh) ^ lz;
+      const half8 a0 = __builtin_bit_cast(half8, sa[lz * 32 + c]);
+      const half8 a1 = __builtin_bit_cast(half8, sa[(32 + lz) * 32 + c]);
       ag0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bg, ag0, 0, 0, 0);
       au0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bu, au0, 0, 0, 0);
       ag1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bg, ag1, 0, 0, 0);
@@ -318,7 +333,7 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
     // block values 0.125 * xd * yd * sum (quantize.rs:763-812), added in superblock order
     const float cg = 0.125f * f16_to_f32_ftz((uint16_t)dg);
     const float cu = 0.125f * f16_to_f32_ftz((uint16_t)du);
-    const float* yd = &s_yd[buf][0];
+    const float* yd = &s_yd[0];
 #pragma unroll
     for (int k = 0; k < 16; k++) {
       const int m = 8 * (k >> 2) + 4 * kh + (k & 3);
@@ -333,22 +348,22 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
   uint32_t gE[17], uE[17], gO[17], uO[17];
   load17(raw_at(grow, 0), gE);
   load17(raw_at(urow, 0), uE);
-  issue_a(0, 0);
+  issue_a(0, std::false_type{});
   for (int b = 0; b < nb; b += 2) {  // nb is even (d is a multiple of 512)
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    issue_a(b + 1, 1);
+    issue_a(b + 1, std::true_type{});
     load17(raw_at(grow, b + 1), gO);
     load17(raw_at(urow, b + 1), uO);
-    superblock(std::true_type{}, 0, gE, uE);
+    superblock(std::true_type{}, gE, uE);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (b + 2 < nb) {
-      issue_a(b + 2, 0);
+      issue_a(b + 2, std::false_type{});
       load17(raw_at(grow, b + 2), gE);
       load17(raw_at(urow, b + 2), uE);
     }
-    superblock(std::false_type{}, 1, gO, uO);
+    superblock(std::false_type{}, gO, uO);
   }
 
   // SwiGLU (utils.rs:141-163) and the routing weight; rows of dead pairs are not stored
@@ -420,9 +435,12 @@ __device__ __forceinline__ half8 q2_half8(uint32_t w0, uint32_t w1, uint32_t shi
 
 extern "C" __global__ __launch_bounds__(kDnThreads)
 void dsmoe_dn_grouped(const DnGroupedArgs a) {
-  __shared__ __align__(16) u32x4 sA[2][kGuBM * 32];    // mid codes, slot m * 32 + (c ^ (m & 31))
-  __shared__ __align__(16) u32x4 sBS[2][kGuBM * 2];    // bsums (int16), two 16-byte halves per pair
-  __shared__ __align__(16) float s_yd[2][kGuBM];
+  // two stage buffers as separate arrays, so the compiler knows that the
+  // direct loads into one do not alias reads of the other (and does not wait
+  // for the next superblock's loads before this one's LDS reads)
+  __shared__ __align__(16) u32x4 sA0[kGuBM * 32], sA1[kGuBM * 32];  // mid codes, slot m * 32 + (c ^ (m & 31))
+  __shared__ __align__(16) u32x4 sBS0[kGuBM * 2], sBS1[kGuBM * 2];  // bsums (int16), two 16-byte halves per pair
+  __shared__ __align__(16) float s_yd0[kGuBM], s_yd1[kGuBM];
   __shared__ uint32_t s_pair[kGuBM], s_mrow[kGuBM], s_qrow[kGuBM];
 
   const TileSlab ts = xcd_tile_slab((int)a.tile_offsets[a.E], a.d / kDnBN);
@@ -453,17 +471,21 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
   }
   // wave 0: block scales (lane = pair); waves 1, 2: bsums halves (lane = pair)
   const uint32_t qoff = s_qrow[lane] + (w == 0 ? 0u : 260u + 16u * (uint32_t)(w - 1));
-  auto issue_a = [&](int b, int buf) {
+  auto issue_a = [&](int b, auto buf_tag) {
+    constexpr bool B1 = decltype(buf_tag)::value;
+    auto& sA = B1 ? sA1 : sA0;
+    auto& sBS = B1 ? sBS1 : sBS0;
+    auto& s_yd = B1 ? s_yd1 : s_yd0;
     const uint8_t* base = (const uint8_t*)a.mh + 512 * b;
 #pragma unroll
     for (int j = 0; j < 4; j++)
-      __builtin_amdgcn_global_load_lds((glb_void*)(base + aoff[j]), (lds_void*)&sA[buf][(4 * w + j) * 64], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((glb_void*)(base + aoff[j]), (lds_void*)&sA[(4 * w + j) * 64], 16, 0, 0);
     if (w == 0)
-      __builtin_amdgcn_global_load_lds((glb_void*)(a.mq + qoff + (size_t)b * Q8K_BYTES), (lds_void*)&s_yd[buf][0], 4,
+      __builtin_amdgcn_global_load_lds((glb_void*)(a.mq + qoff + (size_t)b * Q8K_BYTES), (lds_void*)&s_yd[0], 4,
                                        0, 0);
     else if (w < 3)
       __builtin_amdgcn_global_load_lds((glb_void*)(a.mq + qoff + (size_t)b * Q8K_BYTES),
-                                       (lds_void*)&sBS[buf][64 * (w - 1)], 16, 0, 0);
+                                       (lds_void*)&sBS[64 * (w - 1)], 16, 0, 0);
   };
   const size_t rb = (size_t)nb * Q2K_BYTES;
   const uint8_t* row0 = a.down + ((size_t)e * d + n0 + 32 * w + l32) * rb;
@@ -474,13 +496,17 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) run[q][i] = 0.0f;
 
-  auto superblock = [&](int buf, const uint32_t* r0) {
+  auto superblock = [&](auto buf_tag, const uint32_t* r0) {
+    constexpr bool B1 = decltype(buf_tag)::value;
+    auto& sA = B1 ? sA1 : sA0;
+    auto& sBS = B1 ? sBS1 : sBS0;
+    auto& s_yd = B1 ? s_yd1 : s_yd0;
     float16v acc[2];
 #pragma unroll
     for (int q = 0; q < 2; q++)
 #pragma unroll
       for (int i = 0; i < 16; i++) acc[q][i] = 0.0f;
-    const u32x4* sa = &sA[buf][0];
+    const u32x4* sa = &sA[0];
 #pragma unroll
     for (int ks = 0; ks < 16; ks++) {
       // group ks: codes at piece 2 (ks >> 3) + (ks & 1), shift 2 ((ks & 7) >> 1)
@@ -499,7 +525,7 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
       __builtin_amdgcn_sched_barrier(0);  // one k-step's operands live at a time
     }
     // isum part: + yd * d * isum
-    const float* yd = &s_yd[buf][0];
+    const float* yd = &s_yd[0];
     const float dn0 = f16_to_f32_ftz((uint16_t)(r0[12] & 0xFFFF)), dm0 = f16_to_f32_ftz((uint16_t)(r0[12] >> 16));
 #pragma unroll
     for (int k = 0; k < 16; k++) {
@@ -521,7 +547,7 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
       return __builtin_bit_cast(half8, v);
     };
     auto bsums8 = [&](int m) {  // bsums[m][8 kh .. 8 kh + 7] as f16
-      const u32x4 v = sBS[buf][64 * kh + m];
+      const u32x4 v = sBS[64 * kh + m];
       auto cv = [](uint32_t x) {
         const half2v h = {(_Float16)(float)(int16_t)(x & 0xFFFF), (_Float16)(float)(int16_t)(x >> 16)};
         return __builtin_bit_cast(uint32_t, h);
@@ -545,24 +571,26 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
 
   uint32_t e0[13], o0[13];
   load_q2(row0, kh, e0);
-  issue_a(0, 0);
+  const std::false_type buf0{};
+  const std::true_type buf1{};
+  issue_a(0, buf0);
   for (int b = 0; b < nb; b += 2) {
     const bool odd = b + 1 < nb;  // the odd superblock of this pair exists
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (odd) {
-      issue_a(b + 1, 1);
+      issue_a(b + 1, buf1);
       load_q2(row0 + (size_t)(b + 1) * Q2K_BYTES, kh, o0);
     }
-    superblock(0, e0);
+    superblock(buf0, e0);
     if (!odd) break;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (b + 2 < nb) {
-      issue_a(b + 2, 0);
+      issue_a(b + 2, buf0);
       load_q2(row0 + (size_t)(b + 2) * Q2K_BYTES, kh, e0);
     }
-    superblock(1, o0);
+    superblock(buf1, o0);
   }
 
 #pragma unroll
@@ -886,10 +914,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <bool kSw, int NW>
 __device__ __forceinline__ void q80_wide(const Q80WideArgs& a) {
-  constexpr int SB = 2;            // blocks per stage
+  constexpr int SB = DSM_QW_SB;    // blocks per stage
   constexpr int BT = 64 * NW / 2;  // tokens per workgroup (128 per wave)
-  __shared__ __align__(16) u32x4 sX[2][SB][4 * BT];
-  __shared__ __align__(16) float sS[2][SB][BT];
+  // the two stage buffers are separate arrays: the compiler then knows that
+  // direct loads into one do not alias reads of the other and does not wait
+  // for the next stage's loads before this stage's LDS reads
+  __shared__ __align__(16) u32x4 sX0[SB][4 * BT], sX1[SB][4 * BT];
+  __shared__ __align__(16) float sS0[SB][BT], sS1[SB][BT];
   constexpr int kRows = (kSw ? 16 : 32) * (NW / 2);
   constexpr int NTH = 64 * NW;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -910,15 +941,17 @@ __device__ __forceinline__ void q80_wide(const Q80WideArgs& a) {
     xsrc[h] = (const uint8_t*)(a.xh + (size_t)min(m0 + tl + NTH / 4 * h, T - 1) * in) + 16 * tq;
   // token scales: slot tid < SB * BT = block tid / BT, token tid % BT
   const float* ssrc = a.xs + (size_t)min(m0 + tid % BT, T - 1) * nb + tid / BT;
-  auto issue_x = [&](int st, int buf) {
+  auto issue_x = [&](int st, auto buf_tag) {
+    auto& X = decltype(buf_tag)::value ? sX1 : sX0;
+    auto& S = decltype(buf_tag)::value ? sS1 : sS0;
 #pragma unroll
     for (int j = 0; j < SB; j++)
 #pragma unroll
       for (int h = 0; h < XH; h++)
         __builtin_amdgcn_global_load_lds((glb_void*)(xsrc[h] + 64 * (size_t)(st * SB + j)),
-                                         (lds_void*)&sX[buf][j][64 * w + NTH * h], 16, 0, 0);
+                                         (lds_void*)&X[j][64 * w + NTH * h], 16, 0, 0);
     if (64 * w < SB * BT)
-      __builtin_amdgcn_global_load_lds((glb_void*)(ssrc + st * SB), (lds_void*)(&sS[buf][0][0] + 64 * w), 4, 0, 0);
+      __builtin_amdgcn_global_load_lds((glb_void*)(ssrc + st * SB), (lds_void*)(&S[0][0] + 64 * w), 4, 0, 0);
   };
   // weight tiles of this wave (nt = 0, 1): 16-row tile index
   const int R0 = kSw ? n0 / 16 + rw : n0 / 16 + 2 * rw, R1 = kSw ? R0 : R0 + 1;
@@ -926,17 +959,19 @@ __device__ __forceinline__ void q80_wide(const Q80WideArgs& a) {
   const uint16_t* wh1 = (kSw ? a.w1h : a.w0h) + ((size_t)R1 * nb * 64 + lane) * 8;
   const float* ws0 = a.w0s + (size_t)R0 * nb * 16 + c;
   const float* ws1 = (kSw ? a.w1s : a.w0s) + (size_t)R1 * nb * 16 + c;
-  u32x4 wc[2][SB][2];
-  float wv[2][SB][2];
-  auto load_w = [&](int st, auto buf_tag) {
-    constexpr int buf = decltype(buf_tag)::value;
+  // weights of the next stage land in wn / vn while the current stage runs;
+  // one loop body (no alternating register sets) keeps the running sums in
+  // fixed registers
+  u32x4 wn[SB][2];
+  float vn[SB][2];
+  auto load_w = [&](int st) {
 #pragma unroll
     for (int j = 0; j < SB; j++) {
       const size_t b = (size_t)(st * SB + j);
-      wc[buf][j][0] = *(const u32x4*)(wh0 + b * 512);
-      wc[buf][j][1] = *(const u32x4*)(wh1 + b * 512);
-      wv[buf][j][0] = ws0[b * 16];
-      wv[buf][j][1] = ws1[b * 16];
+      wn[j][0] = *(const u32x4*)(wh0 + b * 512);
+      wn[j][1] = *(const u32x4*)(wh1 + b * 512);
+      vn[j][0] = ws0[b * 16];
+      vn[j][1] = ws1[b * 16];
     }
   };
 
@@ -946,45 +981,63 @@ __device__ __forceinline__ void q80_wide(const Q80WideArgs& a) {
 #pragma unroll
     for (int nt = 0; nt < 2; nt++) run[mt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto compute = [&](auto buf_tag) {
+  // one stage: LDS buffer buf is a compile-time constant, so the compiler
+  // sees that the direct loads into the other buffer do not alias this
+  // stage's reads and does not wait for them
+  auto stage = [&](int st, auto buf_tag) {
     constexpr int buf = decltype(buf_tag)::value;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    u32x4 wc[SB][2];
+    float wv[SB][2];
+#pragma unroll
+    for (int j = 0; j < SB; j++)
+#pragma unroll
+      for (int nt = 0; nt < 2; nt++) { wc[j][nt] = wn[j][nt]; wv[j][nt] = vn[j][nt]; }
+    if (st + 1 < nst) {
+      issue_x(st + 1, std::integral_constant<int, buf ^ 1>{});
+      load_w(st + 1);
+    }
 #pragma unroll
     for (int j = 0; j < SB; j++) {
-      const half8 b0 = __builtin_bit_cast(half8, wc[buf][j][0]), b1 = __builtin_bit_cast(half8, wc[buf][j][1]);
+      const half8 b0 = __builtin_bit_cast(half8, wc[j][0]), b1 = __builtin_bit_cast(half8, wc[j][1]);
+      auto& X = buf ? sX1 : sX0;
+      auto& S = buf ? sS1 : sS0;
+      auto ax_at = [&](int mt) {
+        const int t = 128 * th + 16 * mt + c;
+        return __builtin_bit_cast(half8, X[j][4 * t + (q ^ ((t >> 2) & 3))]);
+      };
+      auto sx_at = [&](int mt) { return *(const f32x4*)&S[j][128 * th + 16 * mt + 4 * q]; };
+      // tile mt + 1's operands are read and its products issued before tile
+      // mt's epilogue, so neither the LDS nor the matrix-core latency is waited out
+      half8 ax = ax_at(0);
+      f32x4 sx = sx_at(0);
+      f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, b0, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+      f32x4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, b1, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
       for (int mt = 0; mt < 8; mt++) {
-        const int t = 128 * th + 16 * mt + c;
-        const half8 ax = __builtin_bit_cast(half8, sX[buf][j][4 * t + (q ^ ((t >> 2) & 3))]);
-        const f32x4 sx = *(const f32x4*)&sS[buf][j][128 * th + 16 * mt + 4 * q];
-        const f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, b0, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-        const f32x4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, b1, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        f32x4 n0v, n1v, nsx;
+        if (mt < 7) {
+          const half8 an = ax_at(mt + 1);
+          nsx = sx_at(mt + 1);
+          n0v = __builtin_amdgcn_mfma_f32_16x16x32_f16(an, b0, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+          n1v = __builtin_amdgcn_mfma_f32_16x16x32_f16(an, b1, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          run[mt][0][i] = __builtin_fmaf(wv[buf][j][0] * sx[i], s0[i], run[mt][0][i]);
-          run[mt][1][i] = __builtin_fmaf(wv[buf][j][1] * sx[i], s1[i], run[mt][1][i]);
+          run[mt][0][i] = __builtin_fmaf(wv[j][0] * sx[i], s0[i], run[mt][0][i]);
+          run[mt][1][i] = __builtin_fmaf(wv[j][1] * sx[i], s1[i], run[mt][1][i]);
         }
+        if (mt < 7) { s0 = n0v; s1 = n1v; sx = nsx; }
       }
     }
   };
-
-  issue_x(0, 0);
-  load_w(0, std::integral_constant<int, 0>{});
+  issue_x(0, std::integral_constant<int, 0>{});
+  load_w(0);
   for (int st = 0; st < nst; st += 2) {  // an odd stage count ends at the break
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (st + 1 < nst) {
-      issue_x(st + 1, 1);
-      load_w(st + 1, std::integral_constant<int, 1>{});
-    }
-    compute(std::integral_constant<int, 0>{});
+    stage(st, std::integral_constant<int, 0>{});
     if (st + 1 >= nst) break;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (st + 2 < nst) {
-      issue_x(st + 2, 0);
-      load_w(st + 2, std::integral_constant<int, 0>{});
-    }
-    compute(std::integral_constant<int, 1>{});
+    stage(st + 1, std::integral_constant<int, 1>{});
   }
 
   // lane l: column (row of the weights) l % 16 of each tile, tokens 4 q .. +3 of each token tile

@@ -281,6 +281,9 @@ struct Q80WideArgs {
 #ifndef DSM_QW_WAVES
 #define DSM_QW_WAVES 8
 #endif
+#ifndef DSM_QW_SB
+#define DSM_QW_SB 2
+#endif
 enum { kQwWaves = DSM_QW_WAVES, kQwBT = 32 * kQwWaves, kQwRows = 16 * kQwWaves, kQwRowsSw = 8 * kQwWaves };
 
 struct SwigluArgs {
