@@ -297,11 +297,13 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) { ag0[i] = 0.0f; ag1[i] = 0.0f; au0[i] = 0.0f; au1[i] = 0.0f; }
     uint32_t g1 = 0, u1 = 0;
-    // the lane index through an opaque copy: the 16 operand addresses below
-    // are formed here, per superblock, not hoisted out of the loop and spilled
-    int lz = l32;
-    asm volatile("" : "+v"(lz));
-    const u32x4* sa = &sA[0];
+    // chunk (2 ks + kh) ^ l32 = (l32 ^ kh) ^ 2 ks: one lane value and an
+    // immediate per k-step.  Both lane values pass through opaque copies, so
+    // the 16 per-step addresses are formed here and not hoisted out of the
+    // loop into registers (at this kernel's register use they would spill)
+    int lk = l32 ^ kh, rowa = l32 * 32;
+    asm volatile("" : "+v"(lk));
+    asm volatile("" : "+v"(rowa));
 #pragma unroll
     for (int ks = 0; ks < 16; ks++) {
       const int sb = ks >> 1;
@@ -322,9 +324,9 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
       };
       const half8 bg = __builtin_bit_cast(half8, u32x4{mul(gv.x, gm.x), mul(gv.y, gm.y), mul(gv.z, gm.z), mul(gv.w, gm.w)});
       const half8 bu = __builtin_bit_cast(half8, u32x4{mul(uv.x, um.x), mul(uv.y, um.y), mul(uv.z, um.z), mul(uv.w, um.w)});
-      const int c = (2 * ks + kh) ^ lz;
-      const half8 a0 = __builtin_bit_cast(half8, sa[lz * 32 + c]);
-      const half8 a1 = __builtin_bit_cast(half8, sa[(32 + lz) * 32 + c]);
+      const int c = lk ^ (2 * ks);
+      const half8 a0 = __builtin_bit_cast(half8, sA[rowa + c]);
+      const half8 a1 = __builtin_bit_cast(half8, sA[rowa + 32 * 32 + c]);
       ag0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bg, ag0, 0, 0, 0);
       au0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bu, au0, 0, 0, 0);
       ag1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bg, ag1, 0, 0, 0);
