@@ -9,7 +9,10 @@ design notes quote).  Reads only CSV files that rocprofv3 wrote (run it with
       scaled by the copy kernel of the benchmark's --copy-calibration (a
       256 MiB device copy: 256 MiB read and 256 MiB written)
   python deepseek-rs_amd/profile_summary.py counters OUT DIR [DIR ...] --title T --cmd C
-      medians per kernel and counter over the dispatches in DIR/*_counter_collection.csv
+      medians per kernel and counter over the dispatches in DIR/*_counter_collection.csv;
+      with SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE in one run also
+      mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDS * GRBM_GUI_ACTIVE / XCDS),
+      the fraction of the dispatch's time the matrix cores were busy
 
 Every table row of a dsmoe kernel carries the hash of the code object it was
 measured on (`code_object=`), so a summary of an older build is recognisable
@@ -24,9 +27,11 @@ import statistics
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 GEMM_PREFIXES = ("dsmoe_gu_grouped", "dsmoe_dn_grouped", "dsmoe_q80_gemm", "dsmoe_q80_combine", "dsmoe_router_tile",
+                 "dsmoe_q80_wide", "dsmoe_q80_unpack",
                  "dsmoe_probe")
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 COPY_KIB = 256 * 1024  # the calibration copy: 256 MiB read and 256 MiB written
+SIMDS, XCDS = 1024, 8  # MI355X: 256 compute units x 4 SIMDs; GRBM_GUI_ACTIVE is summed over the 8 XCDs
 
 
 def code_object_hash(kernel, lib_dir=None):
@@ -111,7 +116,10 @@ def counters(out, dirs, title, cmd):
         for k, cs in sorted(_counters(d).items()):
             if not k.startswith("dsmoe_") or k == "dsmoe_synth":
                 continue
-            vals = "  ".join(f"{c}={statistics.median(v):.4g}" for c, v in sorted(cs.items()))
+            med = {c: statistics.median(v) for c, v in cs.items()}
+            vals = "  ".join(f"{c}={m:.4g}" for c, m in sorted(med.items()))
+            if med.get("GRBM_GUI_ACTIVE") and "SQ_VALU_MFMA_BUSY_CYCLES" in med:
+                vals += f"  mfma_busy={med['SQ_VALU_MFMA_BUSY_CYCLES'] / (SIMDS * med['GRBM_GUI_ACTIVE'] / XCDS):.3f}"
             lines.append(f"{k}  code_object={code_object_hash(k) or '-'}  {vals}")
     open(out, "w").write("\n".join(lines) + "\n")
 
