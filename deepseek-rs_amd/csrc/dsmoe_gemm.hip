@@ -1105,7 +1105,9 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_router_tile(const Router
   uint16_t wh[2][NE];
   float xv[2][NT];
   auto load = [&](int buf, int j) {
-    const int jj = j < nb ? j : 0;
+    // wave-uniform, and declared so: a scalar offset held in a vector
+    // register would wrap every load in a waterfall loop
+    const int jj = __builtin_amdgcn_readfirstlane(j < nb ? j : 0);
 #pragma unroll
     for (int k = 0; k < NE; k++) wh[buf][k] = __builtin_amdgcn_raw_buffer_load_b16(rw, (int)wo[k], 512 * jj, 0);
 #pragma unroll
