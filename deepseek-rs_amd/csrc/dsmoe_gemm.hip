@@ -509,15 +509,26 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; i++) acc[q][i] = 0.0f;
     const u32x4* sa = &sA[0];
+    // the 16 group scales (low nibbles of r0[0..3]) as f16 pairs: each byte
+    // under 0x64 is the f16 1024 + s, less 1024 is s (exact); the offsets
+    // -1024 s of the fma below, two per packed multiply
+    half2v scp[8], ofp[8];
+#pragma unroll
+    for (int wd = 0; wd < 4; wd++) {
+      const uint32_t lo = r0[wd] & 0x0F0F0F0Fu;
+      const half2v bias = {(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
+      scp[2 * wd] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u)) + bias;
+      scp[2 * wd + 1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u)) + bias;
+      ofp[2 * wd] = scp[2 * wd] * bias;
+      ofp[2 * wd + 1] = scp[2 * wd + 1] * bias;
+    }
 #pragma unroll
     for (int ks = 0; ks < 16; ks++) {
       // group ks: codes at piece 2 (ks >> 3) + (ks & 1), shift 2 ((ks & 7) >> 1)
       const int pc = 2 * (ks >> 3) + (ks & 1);
       const uint32_t shift = 2 * ((ks & 7) >> 1);
-      const uint32_t s0 = (r0[ks >> 2] >> (8 * (ks & 3))) & 0xF;
-      const _Float16 f0 = (_Float16)(float)s0;
-      const half2v sc0 = {f0, f0};
-      const half2v of0 = {(_Float16)(-1024.0f) * f0, (_Float16)(-1024.0f) * f0};
+      const half2v sc0 = {scp[ks >> 1][ks & 1], scp[ks >> 1][ks & 1]};
+      const half2v of0 = {ofp[ks >> 1][ks & 1], ofp[ks >> 1][ks & 1]};
       const half8 b0 = q2_half8(r0[4 + 2 * pc], r0[5 + 2 * pc], shift, sc0, of0);
       const int c = (2 * ks + kh) ^ l32;
       const half8 a0 = __builtin_bit_cast(half8, sa[l32 * 32 + c]);
@@ -526,19 +537,14 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
       acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b0, acc[1], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);  // one k-step's operands live at a time
     }
-    // isum part: + yd * d * isum
     const float* yd = &s_yd[0];
     const float dn0 = f16_to_f32_ftz((uint16_t)(r0[12] & 0xFFFF)), dm0 = f16_to_f32_ftz((uint16_t)(r0[12] >> 16));
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-      const int m = 8 * (k >> 2) + 4 * kh + (k & 3);
-      run[0][k] = __builtin_fmaf(yd[m] * dn0, acc[0][k], run[0][k]);
-      run[1][k] = __builtin_fmaf(yd[32 + m] * dn0, acc[1][k], run[1][k]);
-    }
     // summs = bsums . min over the 16 groups: one K = 16 product per tile
     // (bsums |.| <= 16 * 128 and the 4-bit mins are exact in f16)
     auto mins8 = [&](const uint32_t* r) {  // min_j for j = 8 kh .. 8 kh + 7
-      const uint32_t m0 = (r[0 + 2 * kh] >> 4) & 0x0F0F0F0Fu, m1 = (r[1 + 2 * kh] >> 4) & 0x0F0F0F0Fu;
+      // kh varies by lane: a two-way select (an index into r would make a
+      // select chain over all of r's registers)
+      const uint32_t m0 = ((kh ? r[2] : r[0]) >> 4) & 0x0F0F0F0Fu, m1 = ((kh ? r[3] : r[1]) >> 4) & 0x0F0F0F0Fu;
       const half2v off = {(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
       auto cv = [&](uint32_t x) { return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, x) + off); };
       u32x4 v;
@@ -558,16 +564,20 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
     };
     const half8 mn0 = mins8(r0);
     const half8 bs0 = bsums8(l32), bs1 = bsums8(32 + l32);
-    float16v z;
+    float16v z, sm[2];
 #pragma unroll
     for (int i = 0; i < 16; i++) z[i] = 0.0f;
-    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bs0, mn0, z, 0, 0, 0);
-    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bs1, mn0, z, 0, 0, 0);
+    sm[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bs0, mn0, z, 0, 0, 0);
+    sm[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bs1, mn0, z, 0, 0, 0);
+    // block value yd * (d * isum - dmin * summs) (the reference's
+    // dall * isum - dmin' * summs with yd factored out), one multiply and two
+    // fmas per output
+    const float ndm = -dm0;
 #pragma unroll
     for (int k = 0; k < 16; k++) {
       const int m = 8 * (k >> 2) + 4 * kh + (k & 3);
-      run[0][k] = __builtin_fmaf(-(yd[m] * dm0), acc[0][k], run[0][k]);
-      run[1][k] = __builtin_fmaf(-(yd[32 + m] * dm0), acc[1][k], run[1][k]);
+      run[0][k] = __builtin_fmaf(yd[m], __builtin_fmaf(ndm, sm[0][k], dn0 * acc[0][k]), run[0][k]);
+      run[1][k] = __builtin_fmaf(yd[32 + m], __builtin_fmaf(ndm, sm[1][k], dn0 * acc[1][k]), run[1][k]);
     }
   };
 
