@@ -1088,6 +1088,18 @@ extern "C" __global__ __launch_bounds__(64 * kQwWaves) void dsmoe_q80_wide_swigl
 // element 8 experts.
 // grid = ceil(E / 8) * ceil(T / 16), 256 threads.
 // ---------------------------------------------------------------------------
+namespace {
+// f16 bits -> f32 for a product, as f16_to_f32_ftz: the hardware conversion
+// (exact for normal values and Inf), subnormals flushed to a signed zero.  A
+// signalling NaN comes out quiet where the bit-level conversion keeps it
+// signalling; the value only enters a multiply, which quiets it either way,
+// so the products have the same bits.  Four instructions instead of ten.
+__device__ __forceinline__ float f16_to_f32_ftz_hw(uint16_t h) {
+  const float f = (float)__builtin_bit_cast(_Float16, h);
+  return __builtin_fabsf(f) < 6.103515625e-05f ? __builtin_copysignf(0.0f, f) : f;
+}
+}  // namespace
+
 extern "C" __global__ __launch_bounds__(256) void dsmoe_router_tile(const RouterLogitsArgs a) {
   constexpr int NE = 8, NT = 16;
   __shared__ float part[NE * 8][256];  // [expert * 8 + token][tx], eight tokens at a time
@@ -1127,7 +1139,7 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_router_tile(const Router
   auto products = [&](int buf) {
     float wv[NE];
 #pragma unroll
-    for (int k = 0; k < NE; k++) wv[k] = f16_to_f32_ftz_nb(wh[buf][k]);
+    for (int k = 0; k < NE; k++) wv[k] = f16_to_f32_ftz_hw(wh[buf][k]);
 #pragma unroll
     for (int e = 0; e < NE; e++)
 #pragma unroll

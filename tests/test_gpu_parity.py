@@ -79,6 +79,28 @@ def test_router_logits_bitexact(gpu, E, d, T):
     assert bits_equal(np_(out), want)
 
 
+@pytest.mark.parametrize("T", [3, 40])
+def test_router_logits_special_weights_bitexact(gpu, T):
+    """Router weights over the whole finite f16 range with many subnormals
+    (flushed to signed zeros by the reference's conversion) and signed zeros,
+    per-row (T <= 8) and tiled (T > 8) kernels."""
+    import torch
+    E, d = 24, 2048
+    say(f"router_logits special weights T={T}")
+    rng = np.random.default_rng(11)
+    h = rng.integers(0, 0x7C00, size=(E, d), dtype=np.uint16)
+    u = rng.random((E, d))
+    h[u < 0.25] = rng.integers(1, 0x0400, size=int((u < 0.25).sum()), dtype=np.uint16)  # subnormal
+    h[(u >= 0.25) & (u < 0.3)] = 0
+    h |= (rng.random((E, d)) < 0.5).astype(np.uint16) << 15
+    w = torch.from_numpy(h.view(np.int16).copy()).to(gpu)
+    x = dsmoe.synth(dsmoe.FMT_F32, 1, 2, 1, T, d, sigma=1.0, device=gpu)
+    out = torch.empty(T, E, device=gpu)
+    dsmoe.router_logits(w, x, out, d, E, T)
+    want = O.router_logits(h.reshape(-1).copy(), np_(x), d, E, T, NT)
+    assert bits_equal(np_(out), want)
+
+
 @pytest.mark.parametrize("E,k,ng,tg,bias,scale", [(256, 6, 1, 1, False, 1.5), (64, 6, 1, 1, True, 1.5),
                                                   (256, 8, 8, 4, True, 2.5), (256, 8, 8, 4, False, 2.5),
                                                   (16, 3, 4, 2, True, 1.0)])
