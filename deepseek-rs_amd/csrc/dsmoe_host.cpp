@@ -845,6 +845,11 @@ struct dsmoe_ctx {
   uint32_t* g_tile_starts = nullptr;
   float* q80_part = nullptr;     // split shared-expert GEMM partials, [kQ80MaxSplit][min(T, 256)][cols]
   uint16_t* shw_h[3] = {};       // shared gate / up / down unpacked for dsmoe_q80_wide (codes as f16)
+  // Batches on the wide shared-expert path run the shared expert's chain on
+  // `side` (default priority), forked after the prep launch and joined after
+  // the routed down, so its GEMMs fill the routed grouped launches' tails.
+  hipStream_t side = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
   float* shw_s[3] = {};          // their block scales
   // hash routing (dsmoe_set_hash_routing): table [hash_rows][k], token ids [T]
   const int32_t* hash = nullptr;
@@ -1028,6 +1033,10 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
         A(&c->shw_h[m], is * d * 2);
         A(&c->shw_s[m], is * d / 32 * 4);
       }
+      if (rc == DSMOE_OK && (hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) != hipSuccess ||
+                             hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming) != hipSuccess ||
+                             hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming) != hipSuccess))
+        rc = fail(DSMOE_ERR_HIP, "create: side stream or events");
     }
   }
   if (rc != DSMOE_OK) {
@@ -1047,6 +1056,12 @@ int dsmoe_destroy(dsmoe_ctx* c) {
     c->event_pool.push_back(p.second.second);
   }
   for (hipEvent_t e : c->event_pool) (void)hipEventDestroy(e);
+  if (c->side) {
+    (void)hipStreamSynchronize(c->side);
+    (void)hipStreamDestroy(c->side);
+  }
+  if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+  if (c->ev_join) (void)hipEventDestroy(c->ev_join);
   for (void* p : c->allocs) (void)hipFree(p);
   delete c;
   return DSMOE_OK;
@@ -1078,6 +1093,9 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   const bool em = grouped && (int64_t)P <= (int64_t)DSM_TUNE("DSM_EM_MAX_LOAD", kEmMaxLoad) * E && em_fits(cf);
   // Large batches run the shared expert through the unpacked wide GEMM.
   const bool wide = grouped && cf.shared_fmt == 0 && c->shw_h[0] != nullptr && T >= q80_wide_min_t();
+  // the shared expert's chain on the side stream (wide path only)
+  const bool fork = wide && c->side && DSM_TUNE("DSM_SIDE_SHARED", 1);
+  hipStream_t shs = fork ? c->side : (hipStream_t)stream;
   // In the row-streaming path the selection needs no launch of its own:
   // every routed gate/up workgroup runs it for its token.
   const bool up_rows = !grouped && up_rows_fits(d) && (cf.shared_fmt != 0 || q80_rows_fits(d));
@@ -1089,6 +1107,11 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     Q8KArgs q8k{x, c->xq8k, d, T, grouped && !em ? c->xh : nullptr};
     Q80Args q80{x, c->xq80, c->xs80, d, T, grouped ? c->xh80 : nullptr};
     DSM_TRY(prep_impl(&r, &q8k, cf.shared_fmt == 0 ? &q80 : nullptr, stream));
+  }
+  if (fork) {
+    if (hipEventRecord(c->ev_fork, (hipStream_t)stream) != hipSuccess ||
+        hipStreamWaitEvent(c->side, c->ev_fork, 0) != hipSuccess)
+      return fail(DSMOE_ERR_HIP, "forward: fork of the shared-expert stream");
   }
   // 2. routing                                     (session.rs:2010-2058)
   if (!fuse_sel) {
@@ -1152,13 +1175,13 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     }
     if (grouped && cf.shared_fmt == 0) {  // shared expert as a GEMM over the whole batch
       a.sh_work = 0;
-      StageScope sg(c, DSMOE_STAGE_SH_UP, stream);
+      StageScope sg(c, DSMOE_STAGE_SH_UP, shs);
       if (wide) {
         const void* ws[2] = {w->sh_gate, w->sh_up};
         const int rows[2] = {Is, Is}, nbs[2] = {d / 32, d / 32};
-        DSM_TRY(q80_unpack(ws, c->shw_h, c->shw_s, rows, nbs, 2, stream));
+        DSM_TRY(q80_unpack(ws, c->shw_h, c->shw_s, rows, nbs, 2, shs));
         DSM_TRY(q80_wide_impl(c->shw_h[0], c->shw_s[0], c->shw_h[1], c->shw_s[1], c->xh80, c->xs80, c->sh_mid, d, Is,
-                              T, cf.swiglu_clamp, stream));
+                              T, cf.swiglu_clamp, shs));
       } else {
         DSM_TRY(q80_gemm_impl(w->sh_gate, w->sh_up, c->xh80, c->xs80, c->sh_mid, d, Is, T, cf.swiglu_clamp,
                               T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, stream));
@@ -1180,7 +1203,12 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     Q8KArgs qa{c->mid, c->midq, I, P, grouped && !em ? c->mh : nullptr};
     Q8KArgs qb{c->sh_mid, c->sh_midq, Is, T};
     Q80Args q80{c->sh_mid, c->sh_q80, c->sh_s80, Is, T, grouped ? c->shh : nullptr};
-    DSM_TRY(midq_impl(&qa, cf.shared_fmt == 1 ? &qb : nullptr, cf.shared_fmt == 0 ? &q80 : nullptr, stream));
+    if (fork) {  // the shared mid is quantized on the side stream
+      DSM_TRY(midq_impl(&qa, nullptr, nullptr, stream));
+      DSM_TRY(midq_impl(nullptr, nullptr, &q80, c->side));
+    } else {
+      DSM_TRY(midq_impl(&qa, cf.shared_fmt == 1 ? &qb : nullptr, cf.shared_fmt == 0 ? &q80 : nullptr, stream));
+    }
   }
   // 5. routed down (+ slot sum) + shared down      (session.rs:1977-1986, 2129-2153)
   {
@@ -1218,13 +1246,13 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     if (cf.shared_fmt >= 0) { a.sh_tiles = s2.tiles; a.sh_work = T; }
     if (grouped && cf.shared_fmt == 0) {
       a.sh_work = 0;
-      StageScope sg(c, DSMOE_STAGE_SH_DN, stream);
+      StageScope sg(c, DSMOE_STAGE_SH_DN, shs);
       if (wide) {
         const void* ws[1] = {w->sh_down};
         const int rows[1] = {d}, nbs[1] = {Is / 32};
-        DSM_TRY(q80_unpack(ws, c->shw_h + 2, c->shw_s + 2, rows, nbs, 1, stream));
+        DSM_TRY(q80_unpack(ws, c->shw_h + 2, c->shw_s + 2, rows, nbs, 1, shs));
         DSM_TRY(q80_wide_impl(c->shw_h[2], c->shw_s[2], nullptr, nullptr, c->shh, c->sh_s80, shared_out, Is, d, T,
-                              0.0f, stream));
+                              0.0f, shs));
       } else {
         DSM_TRY(q80_gemm_impl(w->sh_down, nullptr, c->shh, c->sh_s80, shared_out, Is, d, T, 0.0f,
                               T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, stream));
@@ -1242,6 +1270,11 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     }
     DSM_TRY(launch(rows ? K_DN_ROWS : K_DN, dim3(a.dn_tiles * a.dn_work + a.sh_tiles * a.sh_work),
                    dim3(rows ? 256 : std::max(s1.block, s2.block)), lds, stream, a));
+  }
+  if (fork) {  // join: the caller's stream sees shared_out complete
+    if (hipEventRecord(c->ev_join, c->side) != hipSuccess ||
+        hipStreamWaitEvent((hipStream_t)stream, c->ev_join, 0) != hipSuccess)
+      return fail(DSMOE_ERR_HIP, "forward: join of the shared-expert stream");
   }
   return DSMOE_OK;
 }
