@@ -1093,8 +1093,10 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   const bool em = grouped && (int64_t)P <= (int64_t)DSM_TUNE("DSM_EM_MAX_LOAD", kEmMaxLoad) * E && em_fits(cf);
   // Large batches run the shared expert through the unpacked wide GEMM.
   const bool wide = grouped && cf.shared_fmt == 0 && c->shw_h[0] != nullptr && T >= q80_wide_min_t();
-  // the shared expert's chain on the side stream (wide path only)
-  const bool fork = wide && c->side && DSM_TUNE("DSM_SIDE_SHARED", 1);
+  // the shared expert's chain on the side stream (wide path only); with
+  // stage profiling on, every stage runs on the caller's stream so each
+  // stage's time is its own
+  const bool fork = wide && c->side && !c->profiling && DSM_TUNE("DSM_SIDE_SHARED", 1);
   hipStream_t shs = fork ? c->side : (hipStream_t)stream;
   // In the row-streaming path the selection needs no launch of its own:
   // every routed gate/up workgroup runs it for its token.

@@ -1978,6 +1978,26 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_moe_sum(const MoeSumArgs
     if (4 * i >= (size_t)a.T * a.d) return;
     const size_t tok = 4 * i / a.d, row = 4 * i % a.d;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (a.k <= 8) {
+      // every slot's load in flight before the first add (each value is read
+      // once: non-temporal); the adds stay in slot order from +0
+      typedef float f4v __attribute__((ext_vector_type(4)));
+      f4v v[8];
+#pragma unroll
+      for (int s = 0; s < 8; s++)
+        if (s < a.k) v[s] = __builtin_nontemporal_load((const f4v*)(a.down + (tok * a.k + s) * a.d + row));
+#pragma unroll
+      for (int s = 0; s < 8; s++) {
+        if (s < a.k) {
+          acc.x = acc.x + v[s].x;
+          acc.y = acc.y + v[s].y;
+          acc.z = acc.z + v[s].z;
+          acc.w = acc.w + v[s].w;
+        }
+      }
+      *(float4*)(a.out + 4 * i) = acc;
+      return;
+    }
     for (int s = 0; s < a.k; s++) {
       const float4 v = *(const float4*)(a.down + (tok * a.k + s) * a.d + row);
       acc.x = acc.x + v.x;

@@ -135,7 +135,11 @@ int dsmoe_set_hash_routing(dsmoe_ctx* ctx, const int32_t* hash, int32_t hash_row
  * reference has no tracing).  When enabled, every stage of the forward is
  * bracketed by hipEvents on the caller's stream; dsmoe_profile_read waits
  * for them and returns the accumulated milliseconds and launch counts per
- * stage (arrays of DSMOE_STAGE_COUNT), optionally resetting them. */
+ * stage (arrays of DSMOE_STAGE_COUNT), optionally resetting them.
+ * Without profiling, batches on the wide shared-expert path run the shared
+ * expert's GEMMs on a second stream of the context, concurrent with the
+ * routed experts; with profiling on, all stages run on the caller's stream,
+ * one after another, so each stage's time is its own. */
 enum {
   DSMOE_STAGE_PREP = 0,   /* router logits + Q8_K(x) + Q8_0(x)            */
   DSMOE_STAGE_SELECT,     /* routing                                      */
