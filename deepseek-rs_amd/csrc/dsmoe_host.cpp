@@ -845,11 +845,13 @@ struct dsmoe_ctx {
   uint32_t* g_tile_starts = nullptr;
   float* q80_part = nullptr;     // split shared-expert GEMM partials, [kQ80MaxSplit][min(T, 256)][cols]
   uint16_t* shw_h[3] = {};       // shared gate / up / down unpacked for dsmoe_q80_wide (codes as f16)
-  // Batches on the wide shared-expert path run the shared expert's chain on
-  // `side` (default priority), forked after the prep launch and joined after
-  // the routed down, so its GEMMs fill the routed grouped launches' tails.
+  // Batches on the wide shared-expert path run the quantization of x and the
+  // shared expert's chain on `side` (default priority), forked before the
+  // router and joined after the routed down: the quantization runs beside
+  // the VALU-bound router, the shared GEMMs fill the routed grouped
+  // launches' tails.  ev_xq orders the routed gate/up after the quantization.
   hipStream_t side = nullptr;
-  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr, ev_xq = nullptr;
   float* shw_s[3] = {};          // their block scales
   // hash routing (dsmoe_set_hash_routing): table [hash_rows][k], token ids [T]
   const int32_t* hash = nullptr;
@@ -1035,7 +1037,8 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
       }
       if (rc == DSMOE_OK && (hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) != hipSuccess ||
                              hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming) != hipSuccess ||
-                             hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming) != hipSuccess))
+                             hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming) != hipSuccess ||
+                             hipEventCreateWithFlags(&c->ev_xq, hipEventDisableTiming) != hipSuccess))
         rc = fail(DSMOE_ERR_HIP, "create: side stream or events");
     }
   }
@@ -1062,6 +1065,7 @@ int dsmoe_destroy(dsmoe_ctx* c) {
   }
   if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
   if (c->ev_join) (void)hipEventDestroy(c->ev_join);
+  if (c->ev_xq) (void)hipEventDestroy(c->ev_xq);
   for (void* p : c->allocs) (void)hipFree(p);
   delete c;
   return DSMOE_OK;
@@ -1102,18 +1106,25 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // every routed gate/up workgroup runs it for its token.
   const bool up_rows = !grouped && up_rows_fits(d) && (cf.shared_fmt != 0 || q80_rows_fits(d));
   const bool fuse_sel = up_rows && !c->hash && DSM_TUNE("DSM_FUSE_SEL", 1);
+  if (fork) {
+    if (hipEventRecord(c->ev_fork, (hipStream_t)stream) != hipSuccess ||
+        hipStreamWaitEvent(c->side, c->ev_fork, 0) != hipSuccess)
+      return fail(DSMOE_ERR_HIP, "forward: fork of the shared-expert stream");
+  }
   // 1. router logits + Q8_K(x) + Q8_0(x)          (session.rs:1894-1909, 1991-2008, 2062-2073)
   {
     StageScope sc(c, DSMOE_STAGE_PREP, stream);
     RouterLogitsArgs r{(const uint16_t*)w->router_f16, x, c->logits, d, E, T};
     Q8KArgs q8k{x, c->xq8k, d, T, grouped && !em ? c->xh : nullptr};
     Q80Args q80{x, c->xq80, c->xs80, d, T, grouped ? c->xh80 : nullptr};
-    DSM_TRY(prep_impl(&r, &q8k, cf.shared_fmt == 0 ? &q80 : nullptr, stream));
-  }
-  if (fork) {
-    if (hipEventRecord(c->ev_fork, (hipStream_t)stream) != hipSuccess ||
-        hipStreamWaitEvent(c->side, c->ev_fork, 0) != hipSuccess)
-      return fail(DSMOE_ERR_HIP, "forward: fork of the shared-expert stream");
+    if (fork) {  // the router here, the quantizations on the side stream
+      DSM_TRY(prep_impl(&r, nullptr, nullptr, stream));
+      DSM_TRY(midq_impl(&q8k, nullptr, &q80, c->side));
+      if (hipEventRecord(c->ev_xq, c->side) != hipSuccess)
+        return fail(DSMOE_ERR_HIP, "forward: event after the quantization of x");
+    } else {
+      DSM_TRY(prep_impl(&r, &q8k, cf.shared_fmt == 0 ? &q80 : nullptr, stream));
+    }
   }
   // 2. routing                                     (session.rs:2010-2058)
   if (!fuse_sel) {
@@ -1155,6 +1166,8 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
                                    c->g_tile_experts, c->g_tile_starts, wts, c->mid, d, I, K, E, P,
                                    em_pairs(), cf.swiglu_clamp, stream));
     } else if (grouped) {
+      if (fork && hipStreamWaitEvent((hipStream_t)stream, c->ev_xq, 0) != hipSuccess)
+        return fail(DSMOE_ERR_HIP, "forward: wait for the quantization of x");
       StageScope sg(c, DSMOE_STAGE_GU_GROUPED, stream);
       DSM_TRY(dsmoe_gate_up_mid_sorted(w->gate, w->up, c->xh, c->xq8k, c->g_sorted, c->g_offsets, c->g_tile_offsets,
                                        c->g_tile_experts, c->g_tile_starts, wts, c->mid, d, I, K, E, P,
