@@ -669,6 +669,48 @@ def test_layer_shared_expert_wide_gemm(gpu, name, T):
     assert np.median(per_row) <= 1e-5, np.median(per_row)
 
 
+def test_layer_shared_expert_side_stream_same_bits(gpu):
+    """Batches on the wide path run the quantization of x and the shared
+    expert on a second stream of the context, forked before the router and
+    joined into the caller's stream at the end; with stage profiling on, the
+    same forward runs every stage on the caller's stream.  Both orders give
+    the same bits, on a non-default caller stream and on two calls in a row
+    (the second one also checks the join: its outputs are read on the caller's
+    stream right after the call)."""
+    import torch
+    T = 1280
+    case = C.with_tokens(C.CASES["c5"], T)
+    say(f"side stream c5 T={T}")
+    w = C.make_weights(case, device=gpu)
+    x = C.make_x(case, T=T, device=gpu)
+    d, k = case.cfg.d_model, case.cfg.top_k
+    layer = dsmoe.MoeLayer(case.cfg, T)
+    s = torch.cuda.Stream()
+    outs = []
+    for profiling in (False, True, False):
+        layer.set_profiling(profiling)
+        so = torch.full((T, d), float("nan"), device=gpu)
+        ro = torch.full((T, d), float("nan"), device=gpu)
+        sel = torch.empty(T, k, dtype=torch.int32, device=gpu)
+        wt = torch.empty(T, k, device=gpu)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            layer.forward(w, x, so, ro, sel, wt, stream=s)
+            # read on the caller's stream: the join must order it after the shared chain
+            got = (so.clone(), ro.clone(), sel.clone())
+        s.synchronize()
+        if profiling:
+            layer.profile_read(reset=True)
+        outs.append([np_(t) for t in got])
+    layer.set_profiling(False)
+    layer.close()
+    assert not np.isnan(outs[0][0]).any() and not np.isnan(outs[0][1]).any()
+    for o in outs[1:]:
+        assert np.array_equal(o[2], outs[0][2]), "routing differs"
+        assert bits_equal(o[0], outs[0][0]), "shared_out differs between the forked and the serial order"
+        assert bits_equal(o[1], outs[0][1]), "routed_out differs between the forked and the serial order"
+
+
 def test_layer_many_experts_batch_on_the_row_path(gpu):
     """n_expert above the dispatch limit (576 > 512, 9 groups of 64): a
     context for 12 tokens has no grouped buffers, so the batch runs the
