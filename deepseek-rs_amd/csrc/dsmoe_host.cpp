@@ -1035,12 +1035,13 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
         A(&c->shw_h[m], is * d * 2);
         A(&c->shw_s[m], is * d / 32 * 4);
       }
-      if (rc == DSMOE_OK && (hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) != hipSuccess ||
-                             hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming) != hipSuccess ||
-                             hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming) != hipSuccess ||
-                             hipEventCreateWithFlags(&c->ev_xq, hipEventDisableTiming) != hipSuccess))
-        rc = fail(DSMOE_ERR_HIP, "create: side stream or events");
     }
+    if (cfg->shared_fmt == 0 && rc == DSMOE_OK &&
+        (hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) != hipSuccess ||
+         hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming) != hipSuccess ||
+         hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming) != hipSuccess ||
+         hipEventCreateWithFlags(&c->ev_xq, hipEventDisableTiming) != hipSuccess))
+      rc = fail(DSMOE_ERR_HIP, "create: side stream or events");
   }
   if (rc != DSMOE_OK) {
     std::string msg = g_err;
@@ -1097,10 +1098,11 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   const bool em = grouped && (int64_t)P <= (int64_t)DSM_TUNE("DSM_EM_MAX_LOAD", kEmMaxLoad) * E && em_fits(cf);
   // Large batches run the shared expert through the unpacked wide GEMM.
   const bool wide = grouped && cf.shared_fmt == 0 && c->shw_h[0] != nullptr && T >= q80_wide_min_t();
-  // the shared expert's chain on the side stream (wide path only); with
+  // the shared expert's chain on the side stream (batches with a Q8_0 shared
+  // expert); with
   // stage profiling on, every stage runs on the caller's stream so each
   // stage's time is its own
-  const bool fork = wide && c->side && !c->profiling && DSM_TUNE("DSM_SIDE_SHARED", 1);
+  const bool fork = grouped && cf.shared_fmt == 0 && c->side && !c->profiling && DSM_TUNE("DSM_SIDE_SHARED", 1);
   hipStream_t shs = fork ? c->side : (hipStream_t)stream;
   // In the row-streaming path the selection needs no launch of its own:
   // every routed gate/up workgroup runs it for its token.
@@ -1160,14 +1162,14 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     a.gu_work = grouped ? 0 : P;
     size_t lds = up_rows ? gate_up_rows_lds(nb) : gate_up_lds(nb, s1.R);
     if (fuse_sel) lds = std::max(lds, select_lds(E));
+    if (fork && hipStreamWaitEvent((hipStream_t)stream, c->ev_xq, 0) != hipSuccess)
+      return fail(DSMOE_ERR_HIP, "forward: wait for the quantization of x");
     if (em) {
       StageScope sg(c, DSMOE_STAGE_GU_GROUPED, stream);
       DSM_TRY(dsmoe_gate_up_mid_em(w->gate, w->up, c->xq8k, c->g_sorted, c->g_offsets, c->g_tile_offsets,
                                    c->g_tile_experts, c->g_tile_starts, wts, c->mid, d, I, K, E, P,
                                    em_pairs(), cf.swiglu_clamp, stream));
     } else if (grouped) {
-      if (fork && hipStreamWaitEvent((hipStream_t)stream, c->ev_xq, 0) != hipSuccess)
-        return fail(DSMOE_ERR_HIP, "forward: wait for the quantization of x");
       StageScope sg(c, DSMOE_STAGE_GU_GROUPED, stream);
       DSM_TRY(dsmoe_gate_up_mid_sorted(w->gate, w->up, c->xh, c->xq8k, c->g_sorted, c->g_offsets, c->g_tile_offsets,
                                        c->g_tile_experts, c->g_tile_starts, wts, c->mid, d, I, K, E, P,
@@ -1199,7 +1201,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
                               T, cf.swiglu_clamp, shs));
       } else {
         DSM_TRY(q80_gemm_impl(w->sh_gate, w->sh_up, c->xh80, c->xs80, c->sh_mid, d, Is, T, cf.swiglu_clamp,
-                              T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, stream));
+                              T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, shs));
       }
     }
     if (fuse_midq) {
@@ -1270,7 +1272,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
                               0.0f, shs));
       } else {
         DSM_TRY(q80_gemm_impl(w->sh_down, nullptr, c->shh, c->sh_s80, shared_out, Is, d, T, 0.0f,
-                              T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, stream));
+                              T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, shs));
       }
     }
     if (rows) {
