@@ -2225,7 +2225,7 @@ extern "C" __global__ __launch_bounds__(1024) void dsmoe_dispatch(const Dispatch
 #pragma unroll
     for (int q = 0; q < kDispBatch; q++) {
       const int p = c0 + 64 * q + lane;
-      int e = p < hi ? a.selected[p] : 0;
+      int e = (c0 + 64 * q < hi && p < hi) ? a.selected[p] : 0;
       if (e < 0 || e >= E) e = 0;  // negative ids map to expert 0 (moe.rs:299-312); ids past E too
       ev[q] = e;
     }
@@ -2235,6 +2235,7 @@ extern "C" __global__ __launch_bounds__(1024) void dsmoe_dispatch(const Dispatch
     load_ids(c0, ev);
 #pragma unroll
     for (int q = 0; q < kDispBatch; q++) {
+      if (c0 + 64 * q >= hi) break;  // wave-uniform: the rest of the batch is past the wave's range
       const int p = c0 + 64 * q + lane;
       const bool live = p < hi;
       const uint64_t pm = peers_of(ev[q], live, nbits);
@@ -2266,6 +2267,7 @@ extern "C" __global__ __launch_bounds__(1024) void dsmoe_dispatch(const Dispatch
     load_ids(c0, ev);
 #pragma unroll
     for (int q = 0; q < kDispBatch; q++) {
+      if (c0 + 64 * q >= hi) break;
       const int p = c0 + 64 * q + lane, e = ev[q];
       const bool live = p < hi;
       const uint64_t pm = peers_of(e, live, nbits);
