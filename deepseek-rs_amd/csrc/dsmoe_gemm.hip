@@ -1100,9 +1100,13 @@ __device__ __forceinline__ float f16_to_f32_ftz_hw(uint16_t h) {
 }
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256) void dsmoe_router_tile(const RouterLogitsArgs a) {
-  constexpr int NE = 8, NT = 16;
-  __shared__ float part[NE * 8][256];  // [expert * 8 + token][tx], eight tokens at a time
+// NE experts x NT tokens per workgroup (NT a multiple of 8): 8 x 16 for
+// large batches; 4 x 8 for small ones, where the grid of 8 x 16 tiles leaves
+// most compute units idle and the launch lasts one workgroup's time.
+template <int NE, int NT>
+__device__ __forceinline__ void router_tile(const RouterLogitsArgs& a) {
+  constexpr int NR = NE * 8;  // tree rows per half
+  __shared__ float part[NR][256];  // [expert * 8 + token][tx], eight tokens at a time
   const int neg = (a.E + NE - 1) / NE;
   const int e0 = (blockIdx.x % neg) * NE, t0 = (blockIdx.x / neg) * NT;
   const int tx = threadIdx.x, d = a.d, nb = d >> 8;
@@ -1165,18 +1169,21 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_router_tile(const Router
       for (int t = 0; t < 8; t++) part[8 * e + t][tx] = acc[e][8 * h + t];
     __syncthreads();
     for (int s2 = 128, lg = 7; s2 > 0; s2 >>= 1, lg--) {
-      for (int idx = tx; idx < 64 * s2; idx += 256) {
+      for (int idx = tx; idx < NR * s2; idx += 256) {
         const int pr = idx >> lg, i = idx & (s2 - 1);
         part[pr][i] += part[pr][i + s2];
       }
       __syncthreads();
     }
-    if (tx < 64) {
+    if (tx < NR) {
       const int e = tx >> 3, t = 8 * h + (tx & 7);
       if (e0 + e < a.E && t0 + t < a.T) a.out[(size_t)(t0 + t) * a.E + e0 + e] = part[tx][0];
     }
   }
 }
+
+extern "C" __global__ __launch_bounds__(256) void dsmoe_router_tile(const RouterLogitsArgs a) { router_tile<8, 16>(a); }
+extern "C" __global__ __launch_bounds__(256) void dsmoe_router_tile_s(const RouterLogitsArgs a) { router_tile<4, 8>(a); }
 
 
 // ---------------------------------------------------------------------------

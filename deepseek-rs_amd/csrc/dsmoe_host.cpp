@@ -85,7 +85,7 @@ enum Kern { K_PREP, K_ROUTER_SELECT, K_UP, K_MIDQ, K_DN, K_SWIGLU, K_MOE_SUM, K_
             K_GU_GROUPED, K_DN_GROUPED, K_Q80_GEMM_SWIGLU, K_Q80_GEMM,
             K_ROUTER_TILE, K_UP_ROWS, K_DN_ROWS, K_Q80_GEMM_SWIGLU_J7, K_Q80_GEMM_J7, K_Q80_GEMM_SWIGLU_J2,
             K_Q80_GEMM_J2, K_HC_EXPAND, K_PROBE_MFMA, K_PROBE_READ, K_UP_EM, K_DN_EM, K_Q80_COMBINE, K_SELECT_HASH, K_RMS_NORM, K_HC_SPLIT_NORM,
-            K_Q80_UNPACK, K_Q80_WIDE, K_Q80_WIDE_SW, K_COUNT };
+            K_Q80_UNPACK, K_Q80_WIDE, K_Q80_WIDE_SW, K_ROUTER_TILE_S, K_COUNT };
 const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_up", "dsmoe_midq", "dsmoe_dn",
                                    "dsmoe_swiglu", "dsmoe_moe_sum", "dsmoe_dispatch", "dsmoe_synth",
                                    "dsmoe_gu_grouped", "dsmoe_dn_grouped", "dsmoe_q80_gemm_swiglu", "dsmoe_q80_gemm",
@@ -95,10 +95,10 @@ const char* kKernNames[K_COUNT] = {"dsmoe_prep", "dsmoe_router_select", "dsmoe_u
                                    "dsmoe_probe_mfma", "dsmoe_probe_read", "dsmoe_up_em", "dsmoe_dn_em",
                                    "dsmoe_q80_combine", "dsmoe_router_select_hash",
                                    "dsmoe_rms_norm_plain", "dsmoe_hc_split_norm", "dsmoe_q80_unpack", "dsmoe_q80_wide",
-                                   "dsmoe_q80_wide_swiglu"};
+                                   "dsmoe_q80_wide_swiglu", "dsmoe_router_tile_s"};
 // code object of each kernel: 0 = dsmoe_kernels.hsaco, 1 = dsmoe_gemm.hsaco (same directory)
 const int kKernModule[K_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0, 1, 1, 0, 0, 1, 0, 0, 0,
-                                  1, 1, 1};
+                                  1, 1, 1, 1};
 static_assert(DSMOE_GROUPED_TILE_M == kGuBM, "header and kernels disagree on the grouped tile");
 
 extern "C" int dsmoe_noalloc_setup(void** ptr, size_t* bytes);  // dsmoe_noalloc.hip
@@ -321,7 +321,15 @@ static int prep_impl(const RouterLogitsArgs* r, const Q8KArgs* q8k, const Q80Arg
   // the batch kernel addresses x and the router with 32-bit buffer offsets
   if (r && r->T >= kRouterTileMinT && (int64_t)r->T * r->d * 4 < ((int64_t)1 << 31) &&
       (int64_t)r->E * r->d * 2 < ((int64_t)1 << 31)) {
-    DSM_TRY(launch(K_ROUTER_TILE, dim3(((r->E + 7) / 8) * ((r->T + 15) / 16)), dim3(256), 0, stream, *r));
+    // 8 x 16 tiles unless their grid would leave most compute units idle:
+    // below 128 of them (c3, T = 32: 64) the 4 x 8 tiles measured ~1 % faster
+    // per layer, at 256 (c4, T = 128, where the concurrent shared expert is
+    // the longer chain) ~0.6 % slower
+    const unsigned big = (unsigned)(((r->E + 7) / 8) * ((r->T + 15) / 16));
+    if (big < (unsigned)DSM_TUNE("DSM_ROUTER_SMALL_BELOW", 128))
+      DSM_TRY(launch(K_ROUTER_TILE_S, dim3(((r->E + 3) / 4) * ((r->T + 7) / 8)), dim3(256), 0, stream, *r));
+    else
+      DSM_TRY(launch(K_ROUTER_TILE, dim3(big), dim3(256), 0, stream, *r));
     r = nullptr;
     if (!q8k && !q80) return DSMOE_OK;
   }

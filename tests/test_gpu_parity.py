@@ -67,7 +67,8 @@ def test_synth_device_equals_host(gpu):
 
 
 # ------------------------------------------------------------------ router
-@pytest.mark.parametrize("E,d,T", [(256, 7168, 5), (64, 2048, 1), (256, 7168, 33), (20, 2048, 50), (24, 1280, 17), (22, 1280, 3)])
+@pytest.mark.parametrize("E,d,T", [(256, 7168, 5), (64, 2048, 1), (256, 7168, 33), (20, 2048, 50), (24, 1280, 17), (22, 1280, 3),
+                                   (256, 7168, 300), (30, 2048, 1030)])
 def test_router_logits_bitexact(gpu, E, d, T):
     import torch
     say(f"router_logits E={E} d={d} T={T}")
