@@ -2236,11 +2236,9 @@ extern "C" __global__ __launch_bounds__(1024) void dsmoe_dispatch(const Dispatch
 #pragma unroll
     for (int q = 0; q < kDispBatch; q++) {
       if (c0 + 64 * q >= hi) break;  // wave-uniform: the rest of the batch is past the wave's range
-      const int p = c0 + 64 * q + lane;
-      const bool live = p < hi;
-      const uint64_t pm = peers_of(ev[q], live, nbits);
-      if (live && (pm & lt) == 0) s_cnt[wv][ev[q]] += (uint32_t)__popcll(pm);
-      __builtin_amdgcn_wave_barrier();
+      // counts need no order: one LDS atomic per pair (the ranks of the
+      // scatter pass below keep the order)
+      if (c0 + 64 * q + lane < hi) atomicAdd(&s_cnt[wv][ev[q]], 1u);
     }
   }
   __syncthreads();
