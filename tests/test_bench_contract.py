@@ -34,3 +34,22 @@ def test_roofline_traffic_is_tied_to_the_code_object(tmp_path):
     assert b.measured_traffic("dsmoe_up_rows", "c2", "staged", str(tmp_path)) == 123
     assert b.measured_traffic("dsmoe_dn_rows", "c2", "staged", str(tmp_path)) is None  # stale
     assert b.measured_traffic("dsmoe_prep", "c2", "staged", str(tmp_path)) is None  # not measured
+
+
+def test_committed_traffic_summaries_carry_the_keys_the_bench_reads():
+    """The bench line's roofline.traffic comes from profiles/: the committed
+    summaries must hold lines under exactly the kernel, config and path names
+    the bench looks up (decode c2 on the row-streaming path, prefill c5 on the
+    grouped path), whatever build they were measured on."""
+    b = _bench()
+    want = [("dsmoe_up_rows", "c2", "staged"), ("dsmoe_dn_rows", "c2", "staged"),
+            ("dsmoe_gu_grouped", "c5", "grouped"), ("dsmoe_dn_grouped", "c5", "grouped")]
+    keys = set()
+    for kind, cfg in (("decode", "c2"), ("prefill", "c5")):
+        for line in open(os.path.join(ROOT, "profiles", f"moe_{kind}_{cfg}_traffic.txt")):
+            if line.startswith("traffic "):
+                kv = dict(t.split("=", 1) for t in line.split()[1:])
+                keys.add((kv["kernel"], kv["config"], kv["path"]))
+    for k in want:
+        assert k in keys, k
+    assert b.STAGE_KERNEL["up"] == "dsmoe_up_rows" and b.PREFILL_KERNEL["gu_grouped"] == "dsmoe_gu_grouped"
