@@ -45,7 +45,8 @@ def prefill_bench(case, steps, warmup, dev):
     import dsmoe
     from dsmoe import configs as C
     cfg, T = case.cfg, case.T
-    w = C.make_weights(case, layer=0, device=dev)
+    # the shared expert unpacked once per weight load, as an engine would
+    w = C.make_weights(case, layer=0, device=dev).unpack_shared(cfg)
     xs = [C.make_x(case, T=T, step=s, device=dev) for s in range(2)]
     layer = dsmoe.MoeLayer(cfg, T)
     d, k = cfg.d_model, cfg.top_k
@@ -80,10 +81,16 @@ def prefill_bench(case, steps, warmup, dev):
         rows[name] = row
     dom = max((n for n in rows if "flops" in rows[n]), key=lambda n: rows[n]["avg_us"])
     tot_fl = sum(fl.values())
+    import numpy as np
+    counts = np.bincount(sel.cpu().numpy().reshape(-1), minlength=cfg.n_expert)
     layer.close()
     del w, xs
+    where = ("added to the router logits (router column 0 = f16(-s ln rank), x[:, 0] = 1)" if case.zipf_logit
+             else "added to the selection bias (score space, after sqrt(softplus))")
     return {
-        "workload": f"{case.name}: same layer, T={T} tokens, Zipf({case.zipf}) expert popularity prior",
+        "workload": f"{case.name}: same layer, T={T} tokens, Zipf({case.zipf}) expert popularity prior {where}",
+        "experts_used": int(np.count_nonzero(counts)),
+        "top10_share": round(float(np.sort(counts)[::-1][:10].sum() / counts.sum()), 4),
         "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_step": round(ms, 4), "steps": steps,
         "mfma_flops_per_step": int(tot_fl), "achieved_TFLOPs": round(tot_fl / (ms * 1e-3) / 1e12, 1),
         "frac_of_mfma_peak": round(tot_fl / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
@@ -94,6 +101,8 @@ def prefill_bench(case, steps, warmup, dev):
                      "algorithmic_flops": rows[dom]["flops"],
                      "traffic": measured_traffic(PREFILL_KERNEL[dom], case.name, "grouped")},
         "stages": rows,
+        "stage_mode": "solo: stage profiling runs every stage on the launch stream (no side stream), so each "
+                      "kernel's time is its own; ms_per_step is the layer as run, shared expert forked",
     }
 
 
@@ -205,10 +214,12 @@ def host_info():
     return {"nproc": os.cpu_count(), "cpu_model": model}
 
 
-def config_bench(case, w, steps, warmup, dev):
+def config_bench(case, ws, steps, warmup, dev):
     """Tokens/s of one more config on the same library path, with the
     layer's algorithmic HBM bytes (router, the distinct experts' weights,
-    shared expert) and, for the grouped path, its MFMA flops."""
+    shared expert) and, for the grouped path, its MFMA flops.  `ws` is a list
+    of weight sets the steps rotate over (decode-sized configs get enough
+    copies that a step's weights come from HBM, not the last-level cache)."""
     import numpy as np
     import torch
     import dsmoe
@@ -220,7 +231,7 @@ def config_bench(case, w, steps, warmup, dev):
     so, ro = torch.empty(T, d, device=dev), torch.empty(T, d, device=dev)
     sel = torch.empty(T, k, dtype=torch.int32, device=dev)
     wt = torch.empty(T, k, device=dev)
-    step = lambda i: layer.forward(w, xs[i % len(xs)], so, ro, sel, wt)
+    step = lambda i: layer.forward(ws[i % len(ws)], xs[i % len(xs)], so, ro, sel, wt)
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
@@ -237,7 +248,7 @@ def config_bench(case, w, steps, warmup, dev):
         distinct.append(len(np.unique(sel.cpu().numpy())))
     nd = float(np.mean(distinct))
     lb = layer_bytes(cfg, nd)
-    row = {"T": T, "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_step": round(ms, 4),
+    row = {"T": T, "weights_rotated": len(ws), "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_step": round(ms, 4),
            "distinct_experts": nd, "algorithmic_bytes": int(lb),
            "hbm_frac": round(lb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     if T > 8:
@@ -256,14 +267,15 @@ def host_weights(w):
             "sh_down": f(w.sh_down)}
 
 
-def cpu_baseline(case, hw, xs, seconds, cores):
+def cpu_baseline(case, hw, xs, seconds, cores, tokens=None):
     """The CPU oracle (a restatement of the reference arithmetic) on a
-    bounded sample of the same workload."""
+    bounded sample of the same workload: repeated layer calls over the first
+    `tokens` tokens of each batch (all of them by default), for about
+    `seconds` and at least one call."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_ref as O
-    T = xs[0].shape[0]
-    xh = [x.cpu().numpy() for x in xs]
-    O.moe_forward(case.cfg, hw, xh[0], T, cores)  # warm
+    T = xs[0].shape[0] if tokens is None else min(tokens, xs[0].shape[0])
+    xh = [x[:T].cpu().numpy().copy() for x in xs]
     n = 0
     t0 = time.perf_counter()
     while True:
@@ -273,8 +285,67 @@ def cpu_baseline(case, hw, xs, seconds, cores):
         if el >= seconds or n >= 2000:
             break
     return {"value": n * T / el, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"{n} layer calls x {T} token(s) of config {case.name} in {el:.1f} s "
+            "sample": f"{n} layer call{'s' if n > 1 else ''} x {T} token(s) of config {case.name} in {el:.1f} s "
                       f"(oracle/dsmoe_oracle.c, {cores} thread{'s' if cores > 1 else ''}, layer-0 weights)"}
+
+
+# Tokens per CPU oracle call (every core, 1 thread): c1, c3 and c4 in full at
+# every core; c5 (2048 tokens, ~1 min per call at 16 threads) on its first
+# 64; 1-thread runs on the first 4 tokens of the batch configs.
+CPU_TOKENS = {"c1": (None, None), "c2": (None, None), "c3": (None, 4), "c4": (None, 4), "c5": (64, 4),
+              "c5logit": (64, 4)}
+
+
+def cpu_pair(case, hw, xs, seconds, tokens_n, tokens_1):
+    """The CPU oracle at every host core (the baseline) and at 1 thread, each
+    for about `seconds` on a bounded sample of the config's tokens."""
+    n = os.cpu_count() or 1
+    multi = cpu_baseline(case, hw, xs, seconds, n, tokens_n)
+    one = cpu_baseline(case, hw, xs, seconds, 1, tokens_1)
+    return {"tokens_per_s": round(multi["value"], 3), "threads": n, "sample": multi["sample"],
+            "tokens_per_s_1_thread": round(one["value"], 3), "sample_1_thread": one["sample"]}
+
+
+def cpu_main(case, hw, xs, seconds):
+    """cpu_baseline of the bench line: the oracle at every host core (value,
+    cores) with the 1-thread figure beside it."""
+    nproc = os.cpu_count() or 1
+    tn, t1 = CPU_TOKENS.get(case.name, (None, None))
+    cpu = cpu_baseline(case, hw, xs, seconds, nproc, tn)
+    one = cpu_baseline(case, hw, xs, seconds / 2, 1, t1)
+    cpu["host"] = host_info()
+    cpu["value_1_thread"] = round(one["value"], 3)
+    cpu["sample_1_thread"] = one["sample"]
+    return cpu
+
+
+def case_host_weights(case, hw_full, dev):
+    """Host copies of a config's weights for the CPU oracle.  Configs that
+    share C2's expert tensors (same shape and seed) reuse `hw_full` and take
+    only their own router and bias."""
+    import numpy as np
+    import torch
+    import dsmoe
+    from dsmoe import configs as C
+    if hw_full is not None and case.cfg == C.C2_CFG and case.seed == C.CASES["c2"].seed:
+        E, d = case.cfg.n_expert, case.cfg.d_model
+        seed = case.seed
+        router = dsmoe.synth(dsmoe.FMT_F16, seed, C.TID_ROUTER, 1, E, d, sigma=0.02, device="cpu")
+        bias = dsmoe.synth(dsmoe.FMT_F32, seed, C.TID_BIAS, 1, 1, E, sigma=0.01, device="cpu").reshape(E).clone()
+        if case.zipf > 0 and case.zipf_logit:
+            prior = torch.from_numpy(C.zipf_bias(E, case.zipf, seed)).to(torch.float16)
+            router = router.clone()
+            router[:, 0] = prior.view(torch.int16)
+        elif case.zipf > 0:
+            bias += torch.from_numpy(C.zipf_bias(E, case.zipf, seed))
+        hw = dict(hw_full)
+        hw["router"] = router.numpy().view(np.uint16).reshape(-1).copy()
+        hw["bias"] = bias.numpy().copy()
+        return hw
+    w = C.make_weights(case, layer=0, device=dev)
+    hw = host_weights(w)
+    del w
+    return hw
 
 
 def main():
@@ -288,8 +359,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
-    ap.add_argument("--prefill-config", default="c5",
-                    help="config of the prefill measurement added to the line ('none' to skip)")
+    ap.add_argument("--prefill-config", default="c5,c5logit",
+                    help="configs of the prefill measurement added to the line, comma-separated ('none' to skip); "
+                         "c5 is reported under prefill, the others under prefill_variants")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--other-configs", default="c1,c3,c4",
                     help="configs also timed on the same path, reported under other_configs ('none' to skip)")
@@ -400,10 +472,11 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    prefill = None
-    if args.prefill_config != "none" and args.prefill_config != args.config:
-        print(f"[bench] prefill {args.prefill_config}", file=sys.stderr, flush=True)
-        prefill = prefill_bench(C.CASES[args.prefill_config], args.prefill_steps, 2, dev)
+    prefill = {}
+    if args.prefill_config != "none":
+        for name in [n for n in args.prefill_config.split(",") if n and n != args.config]:
+            print(f"[bench] prefill {name}", file=sys.stderr, flush=True)
+            prefill[name] = prefill_bench(C.CASES[name], args.prefill_steps, 2, dev)
 
     others = {}
     if args.other_configs != "none":
@@ -411,10 +484,13 @@ def main():
             oc = C.CASES[name]
             print(f"[bench] config {name}", file=sys.stderr, flush=True)
             same = oc.cfg == cfg and oc.seed == case.seed and oc.d_ff_real == case.d_ff_real
-            ow = layers[0] if same else C.make_weights(oc, layer=0, device=dev)
+            if same:
+                ow = layers if oc.T <= 8 else layers[:1]
+            else:  # decode-sized configs rotate over enough copies to exceed the 256 MB last-level cache
+                nl = max(1, -(-(512 << 20) // layer_bytes(oc.cfg, oc.cfg.n_expert))) if oc.T <= 8 else 1
+                ow = [C.make_weights(oc, layer=i, device=dev) for i in range(nl)]
             others[name] = config_bench(oc, ow, 50 if oc.T <= 8 else 20, 5, dev)
-            if not same:
-                del ow
+            del ow
 
     peaks = None
     if not args.no_peaks:
@@ -425,11 +501,17 @@ def main():
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         hw = host_weights(layers[0])
-        cpu = cpu_baseline(case, hw, xs, args.cpu_seconds, 1)
-        multi = min(16, os.cpu_count() or 1)
-        cpu_multi = cpu_baseline(case, hw, xs, args.cpu_seconds / 2, multi)
-        cpu["host"] = host_info()
-        cpu[f"value_{multi}_threads"] = round(cpu_multi["value"], 2)
+        cpu = cpu_main(case, hw, xs, args.cpu_seconds)
+        # the same oracle beside every other config's GPU figure
+        for name, row in list(others.items()) + list(prefill.items()):
+            oc = C.CASES[name]
+            print(f"[bench] cpu baseline {name}", file=sys.stderr, flush=True)
+            ohw = case_host_weights(oc, hw, dev)
+            oxs = [C.make_x(oc, T=oc.T, step=s, device="cpu") for s in range(2)]
+            tn, t1 = CPU_TOKENS.get(name, (None, 4))
+            row["cpu"] = cpu_pair(oc, ohw, oxs, args.cpu_seconds / 4, tn, t1)
+            row["gpu_over_cpu"] = round(row["tokens_per_s"] / row["cpu"]["tokens_per_s"], 1)
+            del ohw
 
     out = {
         "metric": "MoE-layer tokens/s & % of HBM/MFMA roofline, decode B=1 and prefill 2048",
@@ -458,7 +540,8 @@ def main():
         "graph_replay": None if graph_ms is None else {
             "ms_per_step": round(graph_ms, 5), "tokens_per_s": round(T / (graph_ms * 1e-3), 1),
             "note": "the same steps captured as HIP graphs (one per weight set and activation slot) and replayed"},
-        "prefill": prefill,
+        "prefill": prefill.get("c5"),
+        "prefill_variants": {n: v for n, v in prefill.items() if n != "c5"},
         "other_configs": others,
         "box_peaks": peaks,
         "cpu_baseline": cpu,

@@ -43,17 +43,24 @@ constexpr uint32_t kMagic = 0x46554747u;  // "GGUF", little-endian
 
 // Bytes of n elements of GGUF type `t` (model.rs:54-85), or 0 for a type the
 // engine does not know.
+// The products are checked: a count whose byte size does not fit 64 bits
+// gives UINT64_MAX, which no file can hold.
 uint64_t type_bytes(int32_t t, uint64_t n) {
+  uint64_t per = 0, blk = 1;
   switch (t) {
-    case DSMOE_GGUF_F32: return n * 4;
-    case DSMOE_GGUF_F16: return n * 2;
-    case DSMOE_GGUF_Q8_0: return (n + 31) / 32 * 34;
-    case DSMOE_GGUF_Q2_K: return (n + 255) / 256 * 84;
-    case DSMOE_GGUF_Q4_K: return (n + 255) / 256 * 144;
-    case DSMOE_GGUF_IQ2_XXS: return (n + 255) / 256 * 66;
-    case DSMOE_GGUF_I32: return n * 4;
+    case DSMOE_GGUF_F32: per = 4; break;
+    case DSMOE_GGUF_F16: per = 2; break;
+    case DSMOE_GGUF_Q8_0: per = 34; blk = 32; break;
+    case DSMOE_GGUF_Q2_K: per = 84; blk = 256; break;
+    case DSMOE_GGUF_Q4_K: per = 144; blk = 256; break;
+    case DSMOE_GGUF_IQ2_XXS: per = 66; blk = 256; break;
+    case DSMOE_GGUF_I32: per = 4; break;
     default: return 0;
   }
+  const uint64_t blocks = n / blk + (n % blk != 0);
+  uint64_t bytes = 0;
+  if (__builtin_mul_overflow(blocks, per, &bytes)) return UINT64_MAX;
+  return bytes;
 }
 bool known_type(uint32_t t) { return t == 0 || t == 1 || t == 8 || t == 10 || t == 12 || t == 16 || t == 26; }
 
@@ -168,21 +175,26 @@ int dsmoe_gguf_open(const char* path, dsmoe_gguf** out) {
     const uint32_t nd = c.u32();
     if (!c.ok || nd > 4) return bad(c.ok ? "tensor '" + t.name + "' has more than 4 dims" : "truncated tensor info");
     uint64_t n = 1;
+    bool wrap = false;
     for (uint32_t k = 0; k < nd; k++) {
       t.dims.push_back(c.u64());
-      n *= t.dims.back();
+      wrap |= __builtin_mul_overflow(n, t.dims.back(), &n);
     }
     const uint32_t ty = c.u32();
     t.offset = c.u64();
     if (!c.ok) return bad("truncated tensor info");
     if (!known_type(ty)) return bad("unknown tensor type " + std::to_string(ty) + " for '" + t.name + "'");
+    if (wrap) return bad("tensor '" + t.name + "' has an element count beyond 64 bits");
     t.type = (int32_t)ty;
     t.bytes = type_bytes(t.type, n);
     g->tensors.push_back(std::move(t));
   }
   g->data_offset = ((uint64_t)c.at + 31) & ~(uint64_t)31;
+  // data_offset + offset + bytes <= size, written so that nothing can wrap
   for (const auto& t : g->tensors)
-    if (g->data_offset + t.offset + t.bytes > g->size) return bad("tensor '" + t.name + "' extends past the end of the file");
+    if (g->data_offset > g->size || t.offset > g->size - g->data_offset ||
+        t.bytes > g->size - g->data_offset - t.offset)
+      return bad("tensor '" + t.name + "' extends past the end of the file");
   *out = g;
   return DSMOE_OK;
 }

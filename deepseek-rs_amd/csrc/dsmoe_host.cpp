@@ -1104,8 +1104,16 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // stream their weights once per chunk of em_pairs() pairs
   // (expert-major matvec) instead of dequantizing them into MFMA tiles.
   const bool em = grouped && (int64_t)P <= (int64_t)DSM_TUNE("DSM_EM_MAX_LOAD", kEmMaxLoad) * E && em_fits(cf);
-  // Large batches run the shared expert through the unpacked wide GEMM.
+  // Large batches run the shared expert through the unpacked wide GEMM, over
+  // the caller's unpacked matrices when the weights carry them (all six
+  // pointers), else over the context's copies unpacked in this call.
   const bool wide = grouped && cf.shared_fmt == 0 && c->shw_h[0] != nullptr && T >= q80_wide_min_t();
+  const bool pre_unpacked = w->sh_codes[0] && w->sh_codes[1] && w->sh_codes[2] && w->sh_scales[0] &&
+                            w->sh_scales[1] && w->sh_scales[2];
+  const uint16_t* const* shw_h = pre_unpacked ? w->sh_codes : (const uint16_t* const*)c->shw_h;
+  const float* const* shw_s = pre_unpacked ? w->sh_scales : (const float* const*)c->shw_s;
+  if (pre_unpacked && (!aligned16(w->sh_codes[0]) || !aligned16(w->sh_codes[1]) || !aligned16(w->sh_codes[2])))
+    return fail(DSMOE_ERR_INVALID, "forward: unpacked shared-expert codes must be 16-byte aligned");
   // the shared expert's chain on the side stream (batches with a Q8_0 shared
   // expert); with
   // stage profiling on, every stage runs on the caller's stream so each
@@ -1202,11 +1210,13 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
       a.sh_work = 0;
       StageScope sg(c, DSMOE_STAGE_SH_UP, shs);
       if (wide) {
-        const void* ws[2] = {w->sh_gate, w->sh_up};
-        const int rows[2] = {Is, Is}, nbs[2] = {d / 32, d / 32};
-        DSM_TRY(q80_unpack(ws, c->shw_h, c->shw_s, rows, nbs, 2, shs));
-        DSM_TRY(q80_wide_impl(c->shw_h[0], c->shw_s[0], c->shw_h[1], c->shw_s[1], c->xh80, c->xs80, c->sh_mid, d, Is,
-                              T, cf.swiglu_clamp, shs));
+        if (!pre_unpacked) {
+          const void* ws[2] = {w->sh_gate, w->sh_up};
+          const int rows[2] = {Is, Is}, nbs[2] = {d / 32, d / 32};
+          DSM_TRY(q80_unpack(ws, c->shw_h, c->shw_s, rows, nbs, 2, shs));
+        }
+        DSM_TRY(q80_wide_impl(shw_h[0], shw_s[0], shw_h[1], shw_s[1], c->xh80, c->xs80, c->sh_mid, d, Is, T,
+                              cf.swiglu_clamp, shs));
       } else {
         DSM_TRY(q80_gemm_impl(w->sh_gate, w->sh_up, c->xh80, c->xs80, c->sh_mid, d, Is, T, cf.swiglu_clamp,
                               T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, shs));
@@ -1273,11 +1283,13 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
       a.sh_work = 0;
       StageScope sg(c, DSMOE_STAGE_SH_DN, shs);
       if (wide) {
-        const void* ws[1] = {w->sh_down};
-        const int rows[1] = {d}, nbs[1] = {Is / 32};
-        DSM_TRY(q80_unpack(ws, c->shw_h + 2, c->shw_s + 2, rows, nbs, 1, shs));
-        DSM_TRY(q80_wide_impl(c->shw_h[2], c->shw_s[2], nullptr, nullptr, c->shh, c->sh_s80, shared_out, Is, d, T,
-                              0.0f, shs));
+        if (!pre_unpacked) {
+          const void* ws[1] = {w->sh_down};
+          const int rows[1] = {d}, nbs[1] = {Is / 32};
+          DSM_TRY(q80_unpack(ws, c->shw_h + 2, c->shw_s + 2, rows, nbs, 1, shs));
+        }
+        DSM_TRY(q80_wide_impl(shw_h[2], shw_s[2], nullptr, nullptr, c->shh, c->sh_s80, shared_out, Is, d, T, 0.0f,
+                              shs));
       } else {
         DSM_TRY(q80_gemm_impl(w->sh_down, nullptr, c->shh, c->sh_s80, shared_out, Is, d, T, 0.0f,
                               T <= 256 ? c->q80_part : nullptr, kQ80MaxSplit, shs));
@@ -1315,6 +1327,22 @@ int dsmoe_forward_noalloc(const dsmoe_config* cfg, const dsmoe_weights* w, const
   DSM_TRY(validate_cfg(cfg));
   if (T < 0 || T > kDecodeMaxT) return fail(DSMOE_ERR_UNSUPPORTED, "forward_noalloc: T must be in 0..8");
   DSM_TRY(layer_fits_lds(*cfg));
+  {
+    // The first call on a device loads the code objects and clears the static
+    // scratch (a launch and a synchronization), which a stream under graph
+    // capture cannot take: that set-up must happen before capture.
+    int dev = 0;
+    DSM_CHECK_HIP(hipGetDevice(&dev));
+    bool loaded = false;
+    {
+      std::lock_guard<std::mutex> lk(g_mu);
+      loaded = dev >= 0 && dev < kMaxDevices && g_dev[dev].loaded;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (!loaded && hipStreamIsCapturing((hipStream_t)stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return fail(DSMOE_ERR_INVALID, "forward_noalloc: the device is not set up yet and the stream is capturing; "
+                                     "call dsmoe_init (or one forward_noalloc) on this device before capture");
+  }
   DeviceState* st = nullptr;
   DSM_TRY(load_device(nullptr, &st));
   dsmoe_ctx c;  // pointers into the static scratch; owns nothing

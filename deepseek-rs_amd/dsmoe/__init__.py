@@ -54,7 +54,8 @@ class Config(ctypes.Structure):
 
 class Weights(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in
-                ("router_f16", "bias", "gate", "up", "down", "sh_gate", "sh_up", "sh_down")]
+                ("router_f16", "bias", "gate", "up", "down", "sh_gate", "sh_up", "sh_down")] + \
+               [("sh_codes", ctypes.c_void_p * 3), ("sh_scales", ctypes.c_void_p * 3)]
 
 
 _lib = None
@@ -314,10 +315,34 @@ class LayerWeights:
     sh_gate: object = None
     sh_up: object = None
     sh_down: object = None
+    sh_unpacked: object = None  # (codes gate, up, down; scales gate, up, down) from unpack_shared
 
     def c(self) -> Weights:
-        return Weights(*[(_p(getattr(self, n)).value or None) for n in
-                         ("router_f16", "bias", "gate", "up", "down", "sh_gate", "sh_up", "sh_down")])
+        w = Weights(*[(_p(getattr(self, n)).value or None) for n in
+                      ("router_f16", "bias", "gate", "up", "down", "sh_gate", "sh_up", "sh_down")])
+        if self.sh_unpacked is not None:
+            for i in range(3):
+                w.sh_codes[i] = _p(self.sh_unpacked[i]).value
+                w.sh_scales[i] = _p(self.sh_unpacked[3 + i]).value
+        return w
+
+    def unpack_shared(self, cfg, stream=None):
+        """Rewrite the Q8_0 shared expert once into the wide GEMM's operand
+        layout (dsmoe_q8_0_unpack) and keep it with these weights: batches of
+        1024 tokens and more then skip the per-call unpack.  The unpacked
+        copies must be redone if the shared-expert bytes change."""
+        import torch
+        if cfg.shared_fmt != 0 or self.sh_gate is None:
+            return self
+        d, Is = cfg.d_model, cfg.d_ff_shared
+        dev = self.sh_gate.device
+        shapes = ((self.sh_gate, Is, d), (self.sh_up, Is, d), (self.sh_down, d, Is))
+        codes = [torch.empty(r * c, dtype=torch.int16, device=dev) for _, r, c in shapes]
+        scales = [torch.empty(r * c // 32, dtype=torch.float32, device=dev) for _, r, c in shapes]
+        for (m, r, cdim), h, s in zip(shapes, codes, scales):
+            check(lib().dsmoe_q8_0_unpack(_p(m), r, cdim, _p(h), _p(s), _stream(stream)))
+        self.sh_unpacked = tuple(codes) + tuple(scales)
+        return self
 
 
 def hc_expand(block_out, block_add, residual_hc, split, out_hc, n_embd, n_hc, T, mix_hc, has_add, stream=None):

@@ -10,8 +10,12 @@ C4        : C2 with T=128 (N(0,0.02) router); C4-tie: identical router rows,
             so every logit ties and selection is decided by the bias and
             the lower-index rule.
 C5        : C2 with T=2048 and a Zipf(1.1) popularity prior over a seeded
-            expert permutation.  The layer's logits are x.W, so the prior
-            enters through the selection bias (-1.1 ln rank).
+            expert permutation, entered through the selection bias
+            (bias += -1.1 ln rank, i.e. in score space after sqrt(softplus)).
+C5LOGIT   : C2 with T=2048 and the same prior added to the router logits
+            themselves: router column 0 holds f16(-1.1 ln rank) and every
+            token's x[0] is 1.0, so logit_e = prior_e + sum_{i>0} W[e,i] x_i
+            (the prior enters the reference's own logit arithmetic).
 REF       : the reference's own layer (engine/src/model.rs:4,15-18,
             session.rs:21): d=4096, E=256, top-6, no groups, scale 1.5, no
             correction bias, I=2048, Q8_0 shared expert I_s=2048.
@@ -40,6 +44,7 @@ class Case:
     bf16_x: bool = True
     router_tie: bool = False
     zipf: float = 0.0
+    zipf_logit: bool = False  # the prior enters the logits (router column 0, x[:, 0] = 1) instead of the bias
     seed: int = 1234
 
 
@@ -55,6 +60,7 @@ CASES = {
     "c4": Case("c4", C2_CFG, T=128, d_ff_real=2048, d_ff_shared_real=2048),
     "c4tie": Case("c4tie", C2_CFG, T=128, d_ff_real=2048, d_ff_shared_real=2048, router_tie=True),
     "c5": Case("c5", C2_CFG, T=2048, d_ff_real=2048, d_ff_shared_real=2048, zipf=1.1),
+    "c5logit": Case("c5logit", C2_CFG, T=2048, d_ff_real=2048, d_ff_shared_real=2048, zipf=1.1, zipf_logit=True),
     "ref": Case("ref", MoeConfig(d_model=4096, d_ff=2048, n_expert=256, top_k=6, n_group=1, topk_group=1,
                                  route_scale=1.5, swiglu_clamp=10.0, has_bias=False, shared_fmt=0,
                                  d_ff_shared=2048), T=1, d_ff_real=2048, d_ff_shared_real=2048),
@@ -81,7 +87,13 @@ def make_weights(case: Case, layer: int = 0, device="cuda") -> LayerWeights:
     else:
         router = synth(FMT_F16, seed, off + TID_ROUTER, 1, E, d, sigma=0.02, device=device)
     bias = synth(FMT_F32, seed, off + TID_BIAS, 1, 1, E, sigma=0.01, device=device).reshape(E).clone()
-    if case.zipf > 0:
+    if case.zipf > 0 and case.zipf_logit:
+        # logits are sum_i W[e,i] x_i and every token has x[0] = 1 (make_x), so
+        # column 0 adds the prior to each expert's logit
+        prior = torch.from_numpy(zipf_bias(E, case.zipf, seed)).to(torch.float16)
+        router = router.clone()
+        router.view(torch.int16).reshape(E, d)[:, 0] = prior.view(torch.int16).to(router.device)
+    elif case.zipf > 0:
         bias += torch.from_numpy(zipf_bias(E, case.zipf, seed)).to(bias.device)
     gate = synth(FMT_IQ2_XXS, seed, off + TID_GATE, E, I, d, rows_real=Ir, sigma=0.02, device=device)
     up = synth(FMT_IQ2_XXS, seed, off + TID_UP, E, I, d, rows_real=Ir, sigma=0.02, device=device)
@@ -108,6 +120,8 @@ def make_x(case: Case, T: int | None = None, step: int = 0, device="cuda"):
     x = x.reshape(T, case.cfg.d_model)
     if case.bf16_x:
         x = x.to(torch.bfloat16).to(torch.float32)
+    if case.zipf_logit:
+        x[:, 0] = 1.0  # carries the router's prior column (make_weights)
     return x.contiguous()
 
 

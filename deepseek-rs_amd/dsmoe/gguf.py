@@ -184,11 +184,36 @@ def moe_layer_tensors(cfg, w, layer=0):
     return out
 
 
-def layer_weights(g, layer, device="cuda"):
-    """LayerWeights on `device` from a GgufFile's MoE tensors of `layer`."""
+def moe_layout(cfg):
+    """GGUF type and dims of each MoE tensor of a layer of shape `cfg` (the
+    layout moe_layer_tensors writes); the bias only when cfg.has_bias."""
+    d, I, E, Is = cfg.d_model, cfg.d_ff, cfg.n_expert, cfg.d_ff_shared
+    out = {"ffn_gate_inp.weight": (F16, [d, E]), "ffn_gate_exps.weight": (IQ2_XXS, [d, I, E]),
+           "ffn_up_exps.weight": (IQ2_XXS, [d, I, E]), "ffn_down_exps.weight": (Q2_K, [I, d, E])}
+    if cfg.has_bias:
+        out["exp_probs_b.bias"] = (F32, [E])
+    if cfg.shared_fmt in (0, 1):
+        a, b = (Q8_0, Q8_0) if cfg.shared_fmt == 0 else (IQ2_XXS, Q2_K)
+        out.update({"ffn_gate_shexp.weight": (a, [d, Is]), "ffn_up_shexp.weight": (a, [d, Is]),
+                    "ffn_down_shexp.weight": (b, [Is, d])})
+    return out
+
+
+def layer_weights(g, layer, cfg, device="cuda"):
+    """LayerWeights on `device` from a GgufFile's MoE tensors of `layer`,
+    after checking every tensor the layer of shape `cfg` needs: present,
+    of the type and dims the kernels read (a mismatch raises ValueError
+    rather than running the layer on bytes of another shape)."""
     import torch
     from . import LayerWeights
     t = g.moe_layer(layer)
+    for name, (ty, dims) in moe_layout(cfg).items():
+        if name not in t:
+            raise ValueError(f"blk.{layer}.{name}: missing")
+        got = t[name]
+        gd = list(got.dims[:got.n_dims])
+        if got.type != ty or gd != dims:
+            raise ValueError(f"blk.{layer}.{name}: type {got.type} dims {gd}, the layer needs type {ty} dims {dims}")
     up = lambda n: None if n not in t else torch.from_numpy(t[n].array()).to(device)
     return LayerWeights(up("ffn_gate_inp.weight"), None if "exp_probs_b.bias" not in t else
                         torch.from_numpy(t["exp_probs_b.bias"].array().view(np.float32)).to(device),

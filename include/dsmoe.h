@@ -75,6 +75,14 @@ typedef struct dsmoe_weights {
   const void* sh_gate;    /* blk.N.ffn_gate_shexp */
   const void* sh_up;      /* blk.N.ffn_up_shexp   */
   const void* sh_down;    /* blk.N.ffn_down_shexp */
+  /* Optional, no reference counterpart: the Q8_0 shared expert's gate, up
+   * and down already rewritten by dsmoe_q8_0_unpack (codes f16 [rows *
+   * in_dim], scales f32 [rows * in_dim / 32]), done once per weight load.
+   * Batches on the wide shared-expert path (T >= 1024) then read these
+   * instead of unpacking the three matrices on every call.  All six NULL
+   * (a zero-initialised struct) = unpack per call. */
+  const uint16_t* sh_codes[3];
+  const float* sh_scales[3];
 } dsmoe_weights;
 
 const char* dsmoe_version(void);
@@ -117,7 +125,10 @@ int dsmoe_forward(dsmoe_ctx* ctx, const dsmoe_weights* w, const float* x, int32_
  * device (dsmoe_init or the first call); a layer whose scratch for 8 tokens
  * exceeds it (or T > 8) is rejected with DSMOE_ERR_UNSUPPORTED.  Same
  * arguments and results as dsmoe_forward.  All calls on one GPU share the
- * array: calls that overlap on one GPU (two streams, two threads) race. */
+ * array: calls that overlap on one GPU (two streams, two threads) race.
+ * Graph capture: the per-device set-up launches a clear and synchronizes,
+ * so it must run before capture (dsmoe_init, or one eager call on that
+ * device); a first call on a capturing stream returns DSMOE_ERR_INVALID. */
 int dsmoe_forward_noalloc(const dsmoe_config* cfg, const dsmoe_weights* w, const float* x, int32_t T,
                           float* shared_out, float* routed_out, int32_t* selected, float* weights,
                           dsmoe_stream_t stream);

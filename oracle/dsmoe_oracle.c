@@ -26,15 +26,20 @@
  *                                  weights sum to route_scale; ratio preservation
  *   grouped routing (n_group > 1)  brute force over all group subsets (no reference
  *                                  counterpart: the reference has no group-limited top-k)
- *   or_router_select_hash          plain-Python restatement of the table lookup on
- *                                  out-of-range tokens and ids (moe.rs:92-109)
+ *   or_router_select_hash          hand-computed weights on a tiny table (logits > 20 are their
+ *                                  own softplus: probabilities 6, 8, 10; an id of -1 weighs 0;
+ *                                  the 2^-14 floor); out-of-range tokens take row 0
+ *                                  (moe.rs:92-159)
  *   or_dispatch                    numpy stable argsort; prefix sums
  *   or_moe_sum                     f32 values whose sum depends on the slot order
  *   or_rms_norm_plain              float64 within f32 rounding; exact on dyadic rows with eps 0
- *   or_hc4_split / or_hc_split_norm float64 restatement (sigmoid, softmax, Sinkhorn, weighted
- *                                  sum, norm) within f32 rounding; the comb's column sums after
- *                                  the last Sinkhorn round; exp bits as or_expf (parity unpinned
- *                                  against the reference GPU's exp)
+ *   or_hc4_split / or_hc_split_norm closed forms: sigmoid(+-ln 3) per section scale; uniform comb
+ *                                  logits with eps = 0.5 follow x <- x / (eps + 4x) once per
+ *                                  column pass and twice per round (pins eps placement and the
+ *                                  round count); a permutation-pattern comb with eps = 0 is
+ *                                  already doubly stochastic (pins the indexing); plus float64
+ *                                  (weighted sum, norm) and Sinkhorn invariants; exp bits as
+ *                                  or_expf (parity unpinned against the reference GPU's exp)
  *   or_hc_expand                   dyadic inputs (exact in f32) vs the float64 formula, with
  *                                  a non-symmetric comb; numpy f32 in the reference's order
  *   or_moe_forward                 float64 dequantise-then-GEMM closed form through the same

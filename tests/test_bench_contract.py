@@ -53,3 +53,23 @@ def test_committed_traffic_summaries_carry_the_keys_the_bench_reads():
     for k in want:
         assert k in keys, k
     assert b.STAGE_KERNEL["up"] == "dsmoe_up_rows" and b.PREFILL_KERNEL["gu_grouped"] == "dsmoe_gu_grouped"
+
+
+def test_cpu_baseline_value_is_the_all_core_run():
+    """cpu_baseline.value is the oracle at every host core (os.cpu_count()),
+    with the 1-thread figure as a side field, on the small config."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "deepseek-rs_amd"))
+    from dsmoe import configs as C
+    b = _bench()
+    case = C.CASES["c1"]
+    w = C.make_weights(case, device="cpu")
+    hw = b.host_weights(w)
+    xs = [C.make_x(case, T=1, step=s, device="cpu") for s in range(2)]
+    cpu = b.cpu_main(case, hw, xs, 0.2)
+    assert cpu["cores"] == os.cpu_count() and cpu["kind"] == "port" and cpu["unit"] == "tokens/s"
+    assert cpu["value"] > 0 and cpu["value_1_thread"] > 0
+    assert f"{os.cpu_count()} threads" in cpu["sample"] and "1 thread" in cpu["sample_1_thread"]
+    pair = b.cpu_pair(case, hw, xs, 0.1, None, None)
+    assert pair["threads"] == os.cpu_count() and pair["tokens_per_s_1_thread"] > 0
+    assert np.isfinite(pair["tokens_per_s"])

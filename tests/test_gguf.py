@@ -167,7 +167,9 @@ def test_metadata_is_walked_and_read(tmp_path):
 
 @pytest.mark.parametrize("case,msg", [("magic", "bad magic"), ("version", "unsupported GGUF version 4"),
                                       ("type", "unknown tensor type 2"), ("kv", "unknown GGUF metadata type 13"),
-                                      ("short", "past the end"), ("trunc", "truncated")])
+                                      ("short", "past the end"), ("trunc", "truncated"),
+                                      ("dims", "beyond 64 bits"), ("offset", "past the end"),
+                                      ("bytes", "past the end")])
 def test_rejected_files(tmp_path, case, msg):
     b = Builder(version=4 if case == "version" else 3, magic=0x12345678 if case == "magic" else 0x46554747)
     if case == "kv":
@@ -181,6 +183,14 @@ def test_rejected_files(tmp_path, case, msg):
         b.u32(2)
         b.buf += bytes(4)  # dims cut short; the file ends inside the tensor info
         b.buf += bytes(16)
+    elif case in ("dims", "offset", "bytes"):
+        # a dims product past 2^64, an offset near 2^64, a byte size past 2^64
+        # (2^62 f32 elements): each would wrap an unchecked end test
+        b.finish_header(1, 0)
+        dims = {"dims": [1 << 33, 1 << 32], "offset": [64], "bytes": [1 << 62]}[case]
+        b.add_tensor("w", 0, dims, (1 << 64) - 64 if case == "offset" else 0)
+        b.align_data()
+        b.buf += bytes(256)
     else:
         b.finish_header(1, 0)
         b.add_tensor("w", 2 if case == "type" else 0, [64], 0)
@@ -212,3 +222,37 @@ def test_moe_layer_round_trip(tmp_path):
             assert got.bytes == len(data)
             assert np.array_equal(got.array(), np.asarray(data, np.uint8))
         assert g.moe_layer(2) == {}
+
+
+@pytest.mark.parametrize("fault", ["router_type", "expert_dims", "missing_shared"])
+def test_layer_weights_checks_types_and_dims(tmp_path, fault):
+    """layer_weights refuses a layer whose tensors do not have the type and
+    dims the kernels read: a router written as F32, experts with another
+    intermediate size, a missing shared expert tensor."""
+    from dsmoe import configs as C
+    case = C.CASES["c1"]
+    cfg = case.cfg
+    w = C.make_weights(case, device="cpu")
+    tensors = G.moe_layer_tensors(cfg, w, layer=0)
+    out = []
+    for name, ty, dims, data in tensors:
+        if fault == "router_type" and name.endswith("ffn_gate_inp.weight"):
+            ty, data = G.F32, np.zeros(dims[0] * dims[1], np.float32).view(np.uint8)
+        if fault == "expert_dims" and name.endswith("ffn_gate_exps.weight"):
+            dims = [dims[0], dims[1] - 256, dims[2]]
+            data = data[:len(data) * dims[1] // (dims[1] + 256)]
+        if fault == "missing_shared" and name.endswith("ffn_down_shexp.weight"):
+            continue
+        out.append((name, ty, dims, data))
+    p = tmp_path / "bad_layer.gguf"
+    G.write(p, out)
+    with G.GgufFile(p) as g:
+        with pytest.raises(ValueError) as ei:
+            G.layer_weights(g, 0, cfg, device="cpu")
+    want = {"router_type": "ffn_gate_inp.weight: type 0", "expert_dims": "ffn_gate_exps.weight: type",
+            "missing_shared": "ffn_down_shexp.weight: missing"}[fault]
+    assert want in str(ei.value)
+    G.write(p, tensors)
+    with G.GgufFile(p) as g:
+        lw = G.layer_weights(g, 0, cfg, device="cpu")
+    assert lw.gate.numel() == w.gate.numel()

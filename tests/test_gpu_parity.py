@@ -632,6 +632,18 @@ def test_layer_c5_zipf_sampled(gpu):
     assert top10 > 0.5
 
 
+def test_layer_c5logit_sampled(gpu):
+    """c5 with the Zipf prior added to the router logits (BASELINE.json's
+    wording) rather than the selection bias: flatter loads over most of the
+    experts, so many partial MFMA tiles; sampled rows against the oracle."""
+    case = C.CASES["c5logit"]
+    sel, _, _ = _run_layer(case, 2048, gpu, sample=_hot_and_cold_rows)
+    counts = np.bincount(sel.reshape(-1), minlength=256)
+    say(f"  c5logit: experts used {np.count_nonzero(counts)}, top-10 share "
+        f"{np.sort(counts)[::-1][:10].sum() / counts.sum():.3f}")
+    assert np.count_nonzero(counts) > 64
+
+
 @pytest.mark.parametrize("name,T", [("ref", 1100), ("c1", 1030)])
 def test_layer_shared_expert_wide_gemm(gpu, name, T):
     """Batches of 1024 tokens and more run the shared expert through the
@@ -653,9 +665,15 @@ def test_layer_shared_expert_wide_gemm(gpu, name, T):
     layer.forward(w, x, so, ro, sel, wt)
     so2 = torch.full((T, d), float("nan"), device=gpu)
     layer.forward(w, x, so2, ro, sel, wt)
+    # the same weights with the shared expert unpacked once (dsmoe_weights.sh_codes)
+    so3 = torch.full((T, d), float("nan"), device=gpu)
+    ro3 = torch.full((T, d), float("nan"), device=gpu)
+    w.unpack_shared(case.cfg)
+    layer.forward(w, x, so3, ro3, sel, wt)
     torch.cuda.synchronize()
     layer.close()
     assert bits_equal(np_(so2), np_(so)), "second call differs"
+    assert bits_equal(np_(so3), np_(so)) and bits_equal(np_(ro3), np_(ro)), "pre-unpacked shared expert differs"
     rows = np.array(sorted(set(range(0, T, 37)) | {255, 256, 1023, 1024, T - 1}))
     so0, _, _, _ = O.moe_forward(case.cfg, _host_weights(w), np_(x)[rows].copy(), len(rows), NT)
     got = np_(so)[rows]
@@ -865,7 +883,7 @@ def test_layer_from_gguf_file(gpu, tmp_path):
     p = tmp_path / "c1.gguf"
     G.write(p, G.moe_layer_tensors(cfg, w, layer=0))
     with G.GgufFile(p) as g:
-        w2 = G.layer_weights(g, 0, device=gpu)
+        w2 = G.layer_weights(g, 0, cfg, device=gpu)
     x = C.make_x(case, T=3, device=gpu)
     outs = []
     for ww in (w, w2):

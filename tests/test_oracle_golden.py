@@ -588,6 +588,80 @@ def test_router_select_hash_restated(oracle):
     assert (sel2 == table[7]).all()
 
 
+def test_router_select_hash_hand_computed(oracle):
+    """Weights worked out by hand on a tiny table (moe.rs:92-159): logits
+    above 20 are their own softplus, so logits 36, 64, 100 give
+    probabilities exactly 6, 8, 10.  Token 1 picks experts (2, 5): sum 14,
+    weights 6 / (14 / 2.5) and 8 / (14 / 2.5).  Token 2 is out of range and
+    takes row 0 = (4, 1).  Row 3 holds an id of -1: it weighs 0 and the other
+    id takes the whole route_scale.  A logit of -100 (exp branch) gives a
+    probability of ~1e-22, far below the 2^-14 floor of the sum, so that row's
+    weights are p / (2^-14 / 2.5)."""
+    E, k, rows, T = 8, 2, 4, 4
+    logits = np.zeros((T, E), np.float32)
+    logits[:, 2], logits[:, 5], logits[:, 4], logits[:, 1] = 36.0, 64.0, 100.0, 0.0
+    logits[:, 6], logits[:, 7] = -100.0, -100.0
+    table = np.array([[4, 1], [2, 5], [6, 7], [-1, 4]], np.int32)
+    tokens = np.array([1, 9, 3, 2], np.int32)
+    probs, sel, w = oracle_ref.router_select_hash(_Cfg(E, k, scale=2.5), logits, table, rows, tokens, 0, T)
+    assert sel.tolist() == [[2, 5], [4, 1], [-1, 4], [6, 7]]
+    assert probs[0, 2] == 6.0 and probs[0, 5] == 8.0 and probs[0, 4] == 10.0
+    assert abs(float(probs[0, 1]) - math.sqrt(math.log(2.0))) < 1e-6
+    f = np.float32
+    assert w[0].tolist() == [f(6) / (f(14) / f(2.5)), f(8) / (f(14) / f(2.5))]
+    assert abs(w[0, 0] - 6 / 5.6) < 1e-6 and abs(w[0, 1] - 8 / 5.6) < 1e-6
+    p1 = f(math.sqrt(math.log(2.0)))
+    s = f(f(10) + probs[0, 1])
+    assert np.allclose(w[1], [10 / (s / 2.5), p1 / (s / 2.5)], rtol=1e-6)
+    assert w[2].tolist() == [0.0, 2.5]
+    tiny = float(probs[0, 6])
+    assert 0 < tiny < 1e-20
+    floor = 2.0 ** -14
+    assert np.allclose(w[3], [tiny / (floor / 2.5), float(probs[0, 7]) / (floor / 2.5)], rtol=1e-6)
+
+
+def test_hc4_split_closed_forms(oracle):
+    """hc4_split_one (hc.rs:17-99) on inputs whose result is known in closed
+    form.  Pre/post: with mix = 1, base = 0 and scales (ln 3, -ln 3, .),
+    pre = sigmoid(ln 3) + eps = 0.75 + eps and post = 2 sigmoid(-ln 3) = 0.5:
+    each section takes its own scale.  Comb with uniform logits and eps = 0.5:
+    every entry follows x <- x / (eps + 4 x), starting from the softmax entry
+    plus eps, once for the initial column pass and twice per further round, so
+    a misplaced eps or a wrong round count gives another number.  Comb with a
+    permutation pattern (logit L at (r, pi(r)), 0 elsewhere) and eps = 0: the
+    row softmax is already doubly stochastic, so every round leaves it as
+    e^L / (e^L + 3) at (r, pi(r)) and 1 / (e^L + 3) elsewhere; pi is not an
+    involution, so a transposed comb fails."""
+    ln3 = math.log(3.0)
+    mix = np.ones(24, np.float32)
+    base = np.zeros(24, np.float32)
+    scale = np.array([ln3, -ln3, 0.0], np.float32)
+    for iters in (1, 2, 3, 7):
+        eps = 0.5
+        got = oracle_ref.hc4_split(mix, scale, base, iters, eps).astype(np.float64)
+        assert np.allclose(got[:4], 0.75 + eps, atol=1e-6) and np.allclose(got[4:8], 0.5, atol=1e-6)
+        x = 0.25 + eps
+        x = x / (eps + 4 * x)
+        for _ in range(iters - 1):
+            x = x / (eps + 4 * x)
+            x = x / (eps + 4 * x)
+        assert np.allclose(got[8:], x, rtol=1e-6), (iters, got[8:], x)
+    pi = [2, 0, 3, 1]
+    L = 3.0
+    m = np.zeros(24, np.float32)
+    for r in range(4):
+        m[8 + 4 * r + pi[r]] = L
+    for iters in (1, 4, 20):
+        got = oracle_ref.hc4_split(m, np.array([0, 0, 1], np.float32), base, iters, 0.0)
+        assert np.array_equal(got[:8], np.array([0.5] * 4 + [1.0] * 4, np.float32))
+        comb = got[8:].astype(np.float64).reshape(4, 4)
+        want = np.full((4, 4), 1 / (math.exp(L) + 3))
+        for r in range(4):
+            want[r, pi[r]] = math.exp(L) / (math.exp(L) + 3)
+        assert np.allclose(comb, want, rtol=2e-6), (iters, comb)
+        assert not np.allclose(comb.T, want, rtol=1e-3)
+
+
 # ---------------------------------------------------------------- HC FFN pre-norm
 def test_rms_norm_plain_reference_tests(oracle):
     """engine/tests/kernels_smoke.rs:306-392: all-equal input gives

@@ -81,3 +81,35 @@ def test_f16_to_f32_ftz_forms_agree(tmp_path):
     nan = ~fin
     exp_bits = ((h[nan].astype(np.uint32) & 0x8000) << 16) | 0x7F800000 | ((h[nan].astype(np.uint32) & 0x3FF) << 13)
     assert np.array_equal(out[nan, 0], exp_bits)
+
+
+def test_c5logit_prior_enters_the_router_logits():
+    """c5logit adds the Zipf prior to the logits themselves: router column 0
+    holds f16(-s ln rank) and x[:, 0] = 1, so each expert's logit is its prior
+    plus the product over the other columns; the correction bias carries no
+    prior (c5 puts it there instead)."""
+    from dataclasses import replace
+    import oracle_ref as O
+    from dsmoe import configs as C
+    small = replace(C.C2_CFG, d_model=512, d_ff=256, n_expert=32, n_group=4, topk_group=2, d_ff_shared=256)
+    base = C.CASES["c5logit"]
+    case = replace(base, cfg=small, T=16, d_ff_real=256, d_ff_shared_real=256)
+    w = C.make_weights(case, device="cpu")
+    x = C.make_x(case, device="cpu").numpy()
+    E, d = small.n_expert, small.d_model
+    prior = C.zipf_bias(E, base.zipf, base.seed).astype(np.float16)
+    router = w.router_f16.numpy().view(np.uint16).reshape(E, d)
+    assert np.array_equal(router[:, 0], prior.view(np.uint16))
+    assert (x[:, 0] == 1.0).all()
+    plain = replace(case, zipf=0.0, zipf_logit=False)
+    wp = C.make_weights(plain, device="cpu")
+    assert np.array_equal(w.bias.numpy(), wp.bias.numpy())  # the bias is the plain N(0, 0.01) one
+    lg = O.router_logits(router.reshape(-1).copy(), x, d, E, case.T, 1)
+    x0 = x.copy()
+    x0[:, 0] = 0.0
+    lg0 = O.router_logits(router.reshape(-1).copy(), x0, d, E, case.T, 1)
+    diff = (lg - lg0).reshape(case.T, E)
+    assert np.allclose(diff, prior.astype(np.float32)[None, :], atol=1e-5)
+    # the bias variant keeps the router and moves the prior into the bias
+    wb = C.make_weights(replace(case, zipf_logit=False), device="cpu")
+    assert np.allclose(wb.bias.numpy() - wp.bias.numpy(), C.zipf_bias(E, base.zipf, base.seed), atol=1e-6)

@@ -73,3 +73,42 @@ def test_noalloc_rejects_more_than_8_tokens(gpu):
                                            dsmoe._p(ro), None, None, None)
     assert rc == 2  # DSMOE_ERR_UNSUPPORTED
     assert b"T must be in 0..8" in dsmoe.lib().dsmoe_last_error()
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """dsmoe_forward_noalloc captured into a HIP graph after the device's
+    set-up (an eager call), replayed several times with eager work and
+    synchronizations between the replays: every replay gives the eager
+    call's bits."""
+    import torch
+    case = C.CASES["c1"]
+    cfg = case.cfg
+    d, k, T = cfg.d_model, cfg.top_k, 2
+    say(f"noalloc graph capture c1 T={T}")
+    w = C.make_weights(case, device=gpu)
+    x = C.make_x(case, T=T, device=gpu)
+    so, ro = torch.empty(T, d, device=gpu), torch.empty(T, d, device=gpu)
+    sel = torch.empty(T, k, dtype=torch.int32, device=gpu)
+    wt = torch.empty(T, k, device=gpu)
+    dsmoe.forward_noalloc(cfg, w, x, so, ro, sel, wt)  # set-up happens here, outside capture
+    torch.cuda.synchronize()
+    want = [_bits(t).copy() for t in (so, ro, sel, wt)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        dsmoe.forward_noalloc(cfg, w, x, so, ro, sel, wt, stream=s)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for t in (so, ro, wt):
+            t.fill_(float("nan"))
+        sel.fill_(-7)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(want, [_bits(t) for t in (so, ro, sel, wt)]):
+            assert np.array_equal(a, b), f"replay {rep} differs from the eager call"
+        dsmoe.forward_noalloc(cfg, w, C.make_x(case, T=T, step=rep + 1, device=gpu), torch.empty_like(so),
+                              torch.empty_like(ro), torch.empty_like(sel), torch.empty_like(wt))
+        torch.cuda.synchronize()
+    del g
