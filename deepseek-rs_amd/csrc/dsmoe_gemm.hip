@@ -384,66 +384,61 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Routed down projection over sorted pairs, weights in registers
+// Routed down projection over sorted pairs on the int8 matrix cores
 // (moe_down_sorted_qwarp32, moe.rs:871-916; block arithmetic
-// quantize.rs:846-901).  A workgroup of 512 is one dispatch tile (up to
-// kGuBM = 64 pairs of one expert) x kDnBN = 256 output rows; wave w computes
-// all 64 pairs x rows n0 + 32w .. +31 as two 32x32 MFMA tiles (small enough
-// for two workgroups, 4 waves per SIMD).
+// quantize.rs:846-901).  A workgroup of kDnThreads = 256 is one dispatch
+// tile (up to kGuBM = 64 pairs of one expert) x kDnBN = 128 output rows;
+// wave w computes all 64 pairs x rows n0 + 32w .. +31 as two 32x32 tiles.
+// Four waves rather than eight: at 168 registers three workgroups share a
+// CU (three waves per SIMD instead of two), 654 -> 540 us at c5.
 //
-// Per superblock: isum = sum_k (sc * q)[n][k] * q8[m][k] on the matrix cores
-// (weights sc * q <= 45 as exact f16, each lane building its own row's
-// operand: 8 two-bit codes -> (1024 + q) as f16 bytes by v_perm, then one
-// packed f16 fma (1024 + q) * sc - 1024 * sc = q * sc, exact), then
-// summs = sum_j bsums[m][j] * min_j[n] as one K = 16 MFMA into the same
-// accumulators; the row sum gets yd * d * isum - yd * dmin * summs, the
-// superblocks of a row in order 0, 1, ... (the reference: per-lane partials
-// and a butterfly; f32 rounding of that order).  Activations (the mid codes
-// as f16) come through LDS one superblock per buffer (direct-to-LDS loads),
-// with the block scales and bsums.
+// Per superblock: isum = sum_k (sc * q)[n][k] * q8[m][k] with
+// v_mfma_i32_32x32x32_i8: the weights sc * q <= 45 and the mid codes
+// |q8| <= 127 are int8, the products and the superblock's sum are exact
+// int32 (|isum| <= 256 * 45 * 127 < 2^22).  k-step s (32 elements) is half
+// s / 4, shift 2 (s % 4) of the Q2_K layout; lane half kh takes elements
+// 16 kh .. 16 kh + 15 of it, i.e. one 16-element group (scale byte 2 s + kh)
+// and the code bytes 32 (s / 4) + 16 kh .. + 15: four dwords shifted and
+// masked to 2-bit selectors, and one v_perm from the group's table
+// sc * (0, 1, 2, 3) turns four codes into four weights.  The activation
+// operand is the same 16 bytes of the pair's int8 codes.  summs =
+// sum_j bsums[m][j] * min_j[n] is one K = 16 f16 MFMA per tile (bsums as
+// f16 from the quantizer, the 4-bit mins exact in f16); the row sum gets
+// yd * (d * isum - dmin * summs), superblocks in order 0, 1, ... (the
+// reference: per-lane partials and a butterfly; f32 rounding of that order).
+//
+// LDS: the 64 pairs' codes of a superblock, rows of 17 16-byte slots (16 of
+// codes and a pad, so the 32 lanes of a k-step read 32 rows of one column
+// without bank conflicts and every address is a lane base plus a constant),
+// loaded straight into LDS by buffer loads; the block scales and bsums the
+// same way.  Two buffers, one superblock ahead.
 // ---------------------------------------------------------------------------
 namespace {
-// 13 words of a Q2_K row's superblock for lane half kh: the scales (words
-// 0-3), the code bytes 16 + 8 kh + 16 p (p = 0..3: words 4 + 2p, 5 + 2p) and
-// d | dmin (word 12)
-__device__ __forceinline__ void load_q2(const uint8_t* blk, int kh, uint32_t* r) {
-  const u32x4 s4 = *(const u32x4*)blk;
-  r[0] = s4.x; r[1] = s4.y; r[2] = s4.z; r[3] = s4.w;
-#pragma unroll
-  for (int p = 0; p < 4; p++) {
-    const uint2 v = *(const uint2*)(blk + 16 + 8 * kh + 16 * p);
-    r[4 + 2 * p] = v.x;
-    r[5 + 2 * p] = v.y;
-  }
-  r[12] = *(const uint32_t*)(blk + 80);
-}
+typedef int int4v __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-// 8 codes (bytes of w0, w1 after shift and mask) times the group scale as f16
-__device__ __forceinline__ half8 q2_half8(uint32_t w0, uint32_t w1, uint32_t shift, half2v sc2, half2v off2) {
-  const uint32_t b0 = (w0 >> shift) & 0x03030303u, b1 = (w1 >> shift) & 0x03030303u;
-  // bytes (q_a, 0x64, q_b, 0x64) are the f16 values 1024 + q; one fused
-  // (1024 + q) * sc - 1024 * sc rounds once, from the exact q * sc
-  auto cv = [&](uint32_t x) {
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2v, x), sc2, off2));
-  };
-  u32x4 v;
-  v.x = cv(__builtin_amdgcn_perm(0x64646464u, b0, 0x04010400u));
-  v.y = cv(__builtin_amdgcn_perm(0x64646464u, b0, 0x04030402u));
-  v.z = cv(__builtin_amdgcn_perm(0x64646464u, b1, 0x04010400u));
-  v.w = cv(__builtin_amdgcn_perm(0x64646464u, b1, 0x04030402u));
-  return __builtin_bit_cast(half8, v);
+constexpr int kDnRowSlots = 17;
+// The 13 dwords of a Q2_K superblock for lane half kh: the scales (words
+// 0-3), the code bytes 16 kh .. 16 kh + 15 of the first half (words 4-7)
+// and 32 + 16 kh .. of the second (8-11), d | dmin (12).
+__device__ __forceinline__ void load_q2_i8(const uint8_t* blk, int kh, uint32_t* r) {
+  const u32x4 s4 = *(const u32x4*)blk;
+  const u32x4 q0 = *(const u32x4*)(blk + 16 + 16 * kh);
+  const u32x4 q1 = *(const u32x4*)(blk + 48 + 16 * kh);
+  r[0] = s4.x; r[1] = s4.y; r[2] = s4.z; r[3] = s4.w;
+  r[4] = q0.x; r[5] = q0.y; r[6] = q0.z; r[7] = q0.w;
+  r[8] = q1.x; r[9] = q1.y; r[10] = q1.z; r[11] = q1.w;
+  r[12] = *(const uint32_t*)(blk + 80);
 }
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(kDnThreads)
 void dsmoe_dn_grouped(const DnGroupedArgs a) {
   // two stage buffers as separate arrays, so the compiler knows that the
-  // direct loads into one do not alias reads of the other (and does not wait
-  // for the next superblock's loads before this one's LDS reads)
-  __shared__ __align__(16) u32x4 sA0[kGuBM * 32], sA1[kGuBM * 32];  // mid codes, slot m * 32 + (c ^ (m & 31))
-  __shared__ __align__(16) u32x4 sBS0[kGuBM * 2], sBS1[kGuBM * 2];  // bsums (int16), two 16-byte halves per pair
+  // direct loads into one do not alias reads of the other
+  __shared__ __align__(16) u32x4 sA0[kGuBM * kDnRowSlots], sA1[kGuBM * kDnRowSlots];
+  __shared__ __align__(16) u32x4 sBS0[kGuBM * 2], sBS1[kGuBM * 2];  // bsums as f16, two halves per pair
   __shared__ __align__(16) float s_yd0[kGuBM], s_yd1[kGuBM];
-  __shared__ uint32_t s_pair[kGuBM], s_mrow[kGuBM], s_qrow[kGuBM];
+  __shared__ uint32_t s_pair[kGuBM], s_mrow[kGuBM], s_qrow[kGuBM], s_brow[kGuBM];
 
   const TileSlab ts = xcd_tile_slab((int)a.tile_offsets[a.E], a.d / kDnBN);
   if (!ts.ok) return;
@@ -460,37 +455,49 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
     const uint32_t pr = tid < cnt ? a.sorted_pairs[p0 + tid] : 0xFFFFFFFFu;
     const uint32_t row = pr != 0xFFFFFFFFu ? pr : 0u;  // dead rows read pair 0, never stored
     s_pair[tid] = pr;
-    s_mrow[tid] = row * (uint32_t)I * 2u;
+    s_mrow[tid] = row * (uint32_t)I;
     s_qrow[tid] = row * (uint32_t)nb * (uint32_t)Q8K_BYTES;
+    s_brow[tid] = row * (uint32_t)(I >> 4) * 2u;
   }
   __syncthreads();
-  // A: 2048 slots of 16 bytes per superblock, four loads per wave
-  uint32_t aoff[4];
+  // A: 64 rows x 17 slots = 17 loads of 64 slots per superblock; wave w
+  // issues loads w, w + 8, w + 16.  Slot sl of load j is pair sl / 17,
+  // column sl % 17 (column 16, the pad, loads column 0 again).
+  constexpr int kLoads = kDnRowSlots;  // 17 wave loads of 64 slots
+  constexpr int kWaves = kDnThreads / 64, kPer = (kLoads + kWaves - 1) / kWaves;
+  uint32_t aoff[kPer];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int sl = (4 * w + j) * 64 + lane, m = sl >> 5, c = (sl & 31) ^ (m & 31);
-    aoff[j] = s_mrow[m] + 16u * (uint32_t)c;
+  for (int jj = 0; jj < kPer; jj++) {
+    const int j = w + kWaves * jj, sl = 64 * j + lane, m = sl / kDnRowSlots, c = sl - kDnRowSlots * m;
+    aoff[jj] = j < kLoads ? s_mrow[m] + 16u * (uint32_t)(c < 16 ? c : 0) : 0u;
   }
-  // wave 0: block scales (lane = pair); waves 1, 2: bsums halves (lane = pair)
-  const uint32_t qoff = s_qrow[lane] + (w == 0 ? 0u : 260u + 16u * (uint32_t)(w - 1));
+  // wave 0: block scales (lane = pair); waves 1, 2: bsum halves (lane = pair)
+  const uint32_t qoff = s_qrow[lane];
+  const uint32_t boff = s_brow[lane] + (w == 2 ? 16u : 0u);
+  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc((void*)a.m8, (short)0, 0x7FFFFFFF, kBufDword3);
   auto issue_a = [&](int b, auto buf_tag) {
     constexpr bool B1 = decltype(buf_tag)::value;
     auto& sA = B1 ? sA1 : sA0;
     auto& sBS = B1 ? sBS1 : sBS0;
     auto& s_yd = B1 ? s_yd1 : s_yd0;
-    const uint8_t* base = (const uint8_t*)a.mh + 512 * b;
+    // the superblock step is the scalar offset (wave-uniform: a vector
+    // offset there would put each load in a waterfall loop)
+    const int sb_off = __builtin_amdgcn_readfirstlane(256 * b);
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-      __builtin_amdgcn_global_load_lds((glb_void*)(base + aoff[j]), (lds_void*)&sA[(4 * w + j) * 64], 16, 0, 0);
+    for (int jj = 0; jj < kPer; jj++)
+      if (w + kWaves * jj < kLoads)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void*)&sA[(w + kWaves * jj) * 64], 16, aoff[jj], sb_off, 0,
+                                                 0);
     if (w == 0)
       __builtin_amdgcn_global_load_lds((glb_void*)(a.mq + qoff + (size_t)b * Q8K_BYTES), (lds_void*)&s_yd[0], 4,
                                        0, 0);
     else if (w < 3)
-      __builtin_amdgcn_global_load_lds((glb_void*)(a.mq + qoff + (size_t)b * Q8K_BYTES),
+      __builtin_amdgcn_global_load_lds((glb_void*)((const uint8_t*)a.bsh + boff + 32u * (uint32_t)b),
                                        (lds_void*)&sBS[64 * (w - 1)], 16, 0, 0);
   };
   const size_t rb = (size_t)nb * Q2K_BYTES;
   const uint8_t* row0 = a.down + ((size_t)e * d + n0 + 32 * w + l32) * rb;
+  const int kh8 = 8 * kh, kh8b = 8 * kh + 16;
 
   float16v run[2];  // pair tiles 0-31, 32-63
 #pragma unroll
@@ -498,91 +505,70 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) run[q][i] = 0.0f;
 
-  auto superblock = [&](auto buf_tag, const uint32_t* r0) {
+  auto superblock = [&](auto buf_tag, const uint32_t* r) {
     constexpr bool B1 = decltype(buf_tag)::value;
     auto& sA = B1 ? sA1 : sA0;
     auto& sBS = B1 ? sBS1 : sBS0;
     auto& s_yd = B1 ? s_yd1 : s_yd0;
-    float16v acc[2];
+    // lane base: row l32 of tile 0, column kh; k-step s adds 2 s columns,
+    // tile 1 adds 32 rows
+    const u32x4* pa = &sA[l32 * kDnRowSlots + kh];
+    int16v acc[2];
 #pragma unroll
     for (int q = 0; q < 2; q++)
 #pragma unroll
-      for (int i = 0; i < 16; i++) acc[q][i] = 0.0f;
-    const u32x4* sa = &sA[0];
-    // the 16 group scales (low nibbles of r0[0..3]) as f16 pairs: each byte
-    // under 0x64 is the f16 1024 + s, less 1024 is s (exact); the offsets
-    // -1024 s of the fma below, two per packed multiply
-    half2v scp[8], ofp[8];
+      for (int i = 0; i < 16; i++) acc[q][i] = 0;
 #pragma unroll
-    for (int wd = 0; wd < 4; wd++) {
-      const uint32_t lo = r0[wd] & 0x0F0F0F0Fu;
-      const half2v bias = {(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
-      scp[2 * wd] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u)) + bias;
-      scp[2 * wd + 1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u)) + bias;
-      ofp[2 * wd] = scp[2 * wd] * bias;
-      ofp[2 * wd + 1] = scp[2 * wd + 1] * bias;
-    }
+    for (int s = 0; s < 8; s++) {
+      const uint32_t* q = r + 4 + 4 * (s >> 2);
+      const uint32_t sh = 2 * (s & 3);
+      // the group's 4-bit scale (byte 2 s + kh of the scales) and its table
+      const uint32_t sc = __builtin_amdgcn_ubfe(r[s >> 1], (s & 1) ? kh8b : kh8, 4);
+      // sc * 0x03020100 as a full-rate 24-bit multiply and a shift (the opaque
+      // copy keeps the compiler from folding them into a 32-bit multiply,
+      // which issues at quarter rate)
+      uint32_t tab = sc * 0x030201u;
+      asm volatile("" : "+v"(tab));
+      tab <<= 8;
+      int4v bv;
 #pragma unroll
-    for (int ks = 0; ks < 16; ks++) {
-      // group ks: codes at piece 2 (ks >> 3) + (ks & 1), shift 2 ((ks & 7) >> 1)
-      const int pc = 2 * (ks >> 3) + (ks & 1);
-      const uint32_t shift = 2 * ((ks & 7) >> 1);
-      const half2v sc0 = {scp[ks >> 1][ks & 1], scp[ks >> 1][ks & 1]};
-      const half2v of0 = {ofp[ks >> 1][ks & 1], ofp[ks >> 1][ks & 1]};
-      const half8 b0 = q2_half8(r0[4 + 2 * pc], r0[5 + 2 * pc], shift, sc0, of0);
-      const int c = (2 * ks + kh) ^ l32;
-      const half8 a0 = __builtin_bit_cast(half8, sa[l32 * 32 + c]);
-      const half8 a1 = __builtin_bit_cast(half8, sa[(32 + l32) * 32 + c]);
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b0, acc[1], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);  // one k-step's operands live at a time
+      for (int i = 0; i < 4; i++) bv[i] = (int)__builtin_amdgcn_perm(tab, tab, (q[i] >> sh) & 0x03030303u);
+      const int4v a0 = __builtin_bit_cast(int4v, pa[2 * s]);
+      const int4v a1 = __builtin_bit_cast(int4v, pa[32 * kDnRowSlots + 2 * s]);
+      acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bv, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bv, acc[1], 0, 0, 0);
     }
-    const float* yd = &s_yd[0];
-    const float dn0 = f16_to_f32_ftz((uint16_t)(r0[12] & 0xFFFF)), dm0 = f16_to_f32_ftz((uint16_t)(r0[12] >> 16));
     // summs = bsums . min over the 16 groups: one K = 16 product per tile
-    // (bsums |.| <= 16 * 128 and the 4-bit mins are exact in f16)
-    auto mins8 = [&](const uint32_t* r) {  // min_j for j = 8 kh .. 8 kh + 7
-      // kh varies by lane: a two-way select (an index into r would make a
-      // select chain over all of r's registers)
-      const uint32_t m0 = ((kh ? r[2] : r[0]) >> 4) & 0x0F0F0F0Fu, m1 = ((kh ? r[3] : r[1]) >> 4) & 0x0F0F0F0Fu;
-      const half2v off = {(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
-      auto cv = [&](uint32_t x) { return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, x) + off); };
-      u32x4 v;
-      v.x = cv(__builtin_amdgcn_perm(0x64646464u, m0, 0x04010400u));
-      v.y = cv(__builtin_amdgcn_perm(0x64646464u, m0, 0x04030402u));
-      v.z = cv(__builtin_amdgcn_perm(0x64646464u, m1, 0x04010400u));
-      v.w = cv(__builtin_amdgcn_perm(0x64646464u, m1, 0x04030402u));
-      return __builtin_bit_cast(half8, v);
-    };
-    auto bsums8 = [&](int m) {  // bsums[m][8 kh .. 8 kh + 7] as f16
-      const u32x4 v = sBS[64 * kh + m];
-      auto cv = [](uint32_t x) {
-        const half2v h = {(_Float16)(float)(int16_t)(x & 0xFFFF), (_Float16)(float)(int16_t)(x >> 16)};
-        return __builtin_bit_cast(uint32_t, h);
-      };
-      return __builtin_bit_cast(half8, u32x4{cv(v.x), cv(v.y), cv(v.z), cv(v.w)});
-    };
-    const half8 mn0 = mins8(r0);
-    const half8 bs0 = bsums8(l32), bs1 = bsums8(32 + l32);
+    // (bsums |.| <= 16 * 127 and the 4-bit mins are exact in f16)
+    // kh varies by lane: a two-way select (an index into r would make a
+    // select chain over all of r's registers)
+    const uint32_t m0 = ((kh ? r[2] : r[0]) >> 4) & 0x0F0F0F0Fu, m1 = ((kh ? r[3] : r[1]) >> 4) & 0x0F0F0F0Fu;
+    const half2v off = {(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
+    auto cv = [&](uint32_t x) { return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, x) + off); };
+    const u32x4 mv = {cv(__builtin_amdgcn_perm(0x64646464u, m0, 0x04010400u)),
+                      cv(__builtin_amdgcn_perm(0x64646464u, m0, 0x04030402u)),
+                      cv(__builtin_amdgcn_perm(0x64646464u, m1, 0x04010400u)),
+                      cv(__builtin_amdgcn_perm(0x64646464u, m1, 0x04030402u))};
+    const half8 mn = __builtin_bit_cast(half8, mv);
     float16v z, sm[2];
 #pragma unroll
     for (int i = 0; i < 16; i++) z[i] = 0.0f;
-    sm[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bs0, mn0, z, 0, 0, 0);
-    sm[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bs1, mn0, z, 0, 0, 0);
+    sm[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, sBS[64 * kh + l32]), mn, z, 0, 0, 0);
+    sm[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, sBS[64 * kh + 32 + l32]), mn, z, 0, 0, 0);
     // block value yd * (d * isum - dmin * summs) (the reference's
-    // dall * isum - dmin' * summs with yd factored out), one multiply and two
-    // fmas per output
-    const float ndm = -dm0;
+    // dall * isum - dmin' * summs with yd factored out)
+    const float dn0 = f16_to_f32_ftz_nb((uint16_t)(r[12] & 0xFFFF)), ndm = -f16_to_f32_ftz_nb((uint16_t)(r[12] >> 16));
+    const float* yd = &s_yd[0];
 #pragma unroll
     for (int k = 0; k < 16; k++) {
       const int m = 8 * (k >> 2) + 4 * kh + (k & 3);
-      run[0][k] = __builtin_fmaf(yd[m], __builtin_fmaf(ndm, sm[0][k], dn0 * acc[0][k]), run[0][k]);
-      run[1][k] = __builtin_fmaf(yd[32 + m], __builtin_fmaf(ndm, sm[1][k], dn0 * acc[1][k]), run[1][k]);
+      run[0][k] = __builtin_fmaf(yd[m], __builtin_fmaf(ndm, sm[0][k], dn0 * (float)acc[0][k]), run[0][k]);
+      run[1][k] = __builtin_fmaf(yd[32 + m], __builtin_fmaf(ndm, sm[1][k], dn0 * (float)acc[1][k]), run[1][k]);
     }
   };
 
   uint32_t e0[13], o0[13];
-  load_q2(row0, kh, e0);
+  load_q2_i8(row0, kh, e0);
   const std::false_type buf0{};
   const std::true_type buf1{};
   issue_a(0, buf0);
@@ -592,7 +578,7 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
     __syncthreads();
     if (odd) {
       issue_a(b + 1, buf1);
-      load_q2(row0 + (size_t)(b + 1) * Q2K_BYTES, kh, o0);
+      load_q2_i8(row0 + (size_t)(b + 1) * Q2K_BYTES, kh, o0);
     }
     superblock(buf0, e0);
     if (!odd) break;
@@ -600,7 +586,7 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
     __syncthreads();
     if (b + 2 < nb) {
       issue_a(b + 2, buf0);
-      load_q2(row0 + (size_t)(b + 2) * Q2K_BYTES, kh, e0);
+      load_q2_i8(row0 + (size_t)(b + 2) * Q2K_BYTES, kh, e0);
     }
     superblock(buf1, o0);
   }

@@ -405,6 +405,16 @@ int dsmoe_q8k_quantize_h(const float* x, void* out, uint16_t* out_h, int32_t in_
   return midq_impl(&a, nullptr, nullptr, stream);
 }
 
+int dsmoe_q8k_quantize_i8(const float* x, void* out, int8_t* out_i8, uint16_t* bsum_h, int32_t in_dim, int32_t rows,
+                          dsmoe_stream_t stream) {
+  if (!x || !out || !out_i8 || !bsum_h) return fail(DSMOE_ERR_INVALID, "q8k_quantize_i8: null pointer");
+  if (in_dim <= 0 || in_dim % 256 || rows < 0)
+    return fail(DSMOE_ERR_INVALID, "q8k_quantize_i8: in_dim must be a multiple of 256");
+  if (!aligned16(out_i8)) return fail(DSMOE_ERR_INVALID, "q8k_quantize_i8: out_i8 must be 16-byte aligned");
+  Q8KArgs a{x, (uint8_t*)out, in_dim, rows, nullptr, out_i8, bsum_h};
+  return midq_impl(&a, nullptr, nullptr, stream);
+}
+
 int dsmoe_q8_0_quantize_h(const float* x, int8_t* xq, float* xscale, uint16_t* out_h, int32_t in_dim, int32_t rows,
                           dsmoe_stream_t stream) {
   if (!x || !xq || !xscale || !out_h) return fail(DSMOE_ERR_INVALID, "q8_0_quantize_h: null pointer");
@@ -630,18 +640,20 @@ int dsmoe_gate_up_mid_sorted(const void* gate, const void* up, const uint16_t* x
   return launch(K_GU_GROUPED, dim3(xcd_grid(max_tiles, I / kGuBN)), dim3(kGuThreads), 0, stream, a);
 }
 
-int dsmoe_down_sorted(const void* down, const uint16_t* mh, const void* mq, const uint32_t* sorted_pairs,
-                      const uint32_t* offsets, const uint32_t* tile_offsets, const uint32_t* tile_experts,
-                      const uint32_t* tile_starts, float* down_out, int32_t d, int32_t I, int32_t E, int32_t pairs,
-                      dsmoe_stream_t stream) {
-  if (!down || !mh || !mq || !sorted_pairs || !offsets || !tile_offsets || !tile_experts || !tile_starts || !down_out)
+int dsmoe_down_sorted(const void* down, const int8_t* m8, const uint16_t* bsum_h, const void* mq,
+                      const uint32_t* sorted_pairs, const uint32_t* offsets, const uint32_t* tile_offsets,
+                      const uint32_t* tile_experts, const uint32_t* tile_starts, float* down_out, int32_t d, int32_t I,
+                      int32_t E, int32_t pairs, dsmoe_stream_t stream) {
+  if (!down || !m8 || !bsum_h || !mq || !sorted_pairs || !offsets || !tile_offsets || !tile_experts || !tile_starts ||
+      !down_out)
     return fail(DSMOE_ERR_INVALID, "down_sorted: null pointer");
-  if (!aligned16(down) || !aligned16(mh)) return fail(DSMOE_ERR_INVALID, "down_sorted: weights and mh must be 16-byte aligned");
+  if (!aligned16(down) || !aligned16(m8) || !aligned16(bsum_h))
+    return fail(DSMOE_ERR_INVALID, "down_sorted: weights, m8 and bsum_h must be 16-byte aligned");
   if (d <= 0 || d % kDnBN || I <= 0 || I % 256 || E <= 0 || pairs < 0)
     return fail(DSMOE_ERR_INVALID, "down_sorted: bad shape");
   if (pairs == 0) return DSMOE_OK;
-  DnGroupedArgs a{(const uint8_t*)down, mh, (const uint8_t*)mq, sorted_pairs, offsets, tile_offsets, tile_experts,
-                  tile_starts, down_out, d, I, E};
+  DnGroupedArgs a{(const uint8_t*)down, m8, bsum_h, (const uint8_t*)mq, sorted_pairs, offsets, tile_offsets,
+                  tile_experts, tile_starts, down_out, d, I, E};
   const int max_tiles = pairs / kGuBM + std::min(E, pairs);
   return launch(K_DN_GROUPED, dim3(xcd_grid(max_tiles, d / kDnBN)), dim3(kDnThreads), 0, stream, a);
 }
@@ -841,7 +853,8 @@ struct dsmoe_ctx {
   float* sh_s80 = nullptr;
   // grouped (sorted-by-expert) path for T > kDecodeMaxT
   uint16_t* xh = nullptr;        // Q8_K(x) qs as f16 [T][d]
-  uint16_t* mh = nullptr;        // Q8_K(mid) qs as f16 [T*k][I]
+  int8_t* m8 = nullptr;          // Q8_K(mid) qs as int8 [T*k][I]
+  uint16_t* bsh = nullptr;       // Q8_K(mid) 16-element sums as f16 [T*k][I/16]
   uint16_t* xh80 = nullptr;      // Q8_0(x) codes as f16 [T][d]
   uint16_t* shh = nullptr;       // Q8_0(shared mid) codes as f16 [T][I_s]
   float* down_out = nullptr;     // [T*k][d]
@@ -1026,7 +1039,8 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
   if (max_tokens > kDecodeMaxT && E <= 512) {
     const size_t P = T * K, max_tiles = P + std::min(E, P);  // dispatch tiles of any block_m >= 1
     A(&c->xh, T * d * 2);
-    A(&c->mh, P * I * 2);
+    A(&c->m8, P * I);
+    A(&c->bsh, P * (I / 16) * 2);
     A(&c->xh80, T * d * 2);
     A(&c->shh, T * Is * 2);
     A(&c->down_out, P * d * 4);
@@ -1235,7 +1249,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // 4. Q8_K(mid) + Q8_0 / Q8_K of the shared mid  (session.rs:1964-1976, 2114-2127)
   if (!fuse_midq) {
     StageScope sc(c, DSMOE_STAGE_MIDQ, stream);
-    Q8KArgs qa{c->mid, c->midq, I, P, grouped && !em ? c->mh : nullptr};
+    Q8KArgs qa{c->mid, c->midq, I, P, nullptr, grouped && !em ? c->m8 : nullptr, grouped && !em ? c->bsh : nullptr};
     Q8KArgs qb{c->sh_mid, c->sh_midq, Is, T};
     Q80Args q80{c->sh_mid, c->sh_q80, c->sh_s80, Is, T, grouped ? c->shh : nullptr};
     if (fork) {  // the shared mid is quantized on the side stream
@@ -1262,7 +1276,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
           DSM_TRY(dsmoe_down_em(w->down, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets, c->g_tile_experts,
                                 c->g_tile_starts, c->down_out, d, I, E, P, em_pairs(), stream));
         } else {
-          DSM_TRY(dsmoe_down_sorted(w->down, c->mh, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets,
+          DSM_TRY(dsmoe_down_sorted(w->down, c->m8, c->bsh, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets,
                                     c->g_tile_experts, c->g_tile_starts, c->down_out, d, I, E, P, stream));
         }
       }

@@ -41,6 +41,8 @@ struct Q8KArgs {
   uint8_t* out;    // [rows][in_dim/256] x 292 B
   int32_t in_dim, rows;
   uint16_t* out_h = nullptr;  // optional: the qs again as f16 [rows][in_dim] (MFMA operand)
+  int8_t* out_8 = nullptr;    // optional: the qs again as int8 [rows][in_dim] (int8 MFMA operand)
+  uint16_t* bsum_h = nullptr; // optional: the 16-element sums as f16 [rows][in_dim/16]
 };
 
 struct Q80Args {
@@ -211,8 +213,9 @@ enum : int32_t { kGuBM = 64, kGuThreads = 512, kGuBN = kGuThreads / 2 };
 // rows (the slot sum is dsmoe_moe_sum).
 struct DnGroupedArgs {
   const uint8_t* down;            // Q2_K [E][d][I/256]
-  const uint16_t* mh;             // Q8_K(mid) qs as f16 [P][I]
-  const uint8_t* mq;              // Q8_K(mid) [P][I/256] (scales, bsums)
+  const int8_t* m8;               // Q8_K(mid) qs as int8 [P][I] (rows 16-byte aligned)
+  const uint16_t* bsh;            // Q8_K(mid) bsums as f16 [P][I/16]
+  const uint8_t* mq;              // Q8_K(mid) [P][I/256] (block scales)
   const uint32_t* sorted_pairs;
   const uint32_t* offsets;
   const uint32_t* tile_offsets;
@@ -221,7 +224,7 @@ struct DnGroupedArgs {
   float* down_out;                // [P][d]
   int32_t d, I, E;
 };
-enum : int32_t { kDnThreads = 512, kDnBN = kDnThreads / 2 };
+enum : int32_t { kDnThreads = 256, kDnBN = kDnThreads / 2 };  // 4 waves: three workgroups per CU at 168 VGPRs
 
 // Dense Q8_0 x Q8_0-activation GEMM for batches (shared expert): tiles of
 // kGuBM tokens x 64 output columns (32 gate + 32 up rows with SwiGLU, or 64

@@ -346,7 +346,13 @@ __device__ __forceinline__ void role_q8k(const Q8KArgs& a, int bx, uint8_t* smem
   }
   s_q[tid] = q;
   if (a.out_h) a.out_h[(size_t)row * a.in_dim + (size_t)b * 256 + tid] = __builtin_bit_cast(uint16_t, (_Float16)q);
+  if (a.out_8) a.out_8[(size_t)row * a.in_dim + (size_t)b * 256 + tid] = q;
   __syncthreads();
+  if (a.bsum_h && tid < 16) {
+    int32_t s = 0;
+    for (int k = 0; k < 16; k++) s += s_q[tid * 16 + k];
+    a.bsum_h[(size_t)row * (a.in_dim >> 4) + (size_t)b * 16 + tid] = __builtin_bit_cast(uint16_t, (_Float16)s);
+  }
   // dword stores: qs (64), bsums (8 words of two int16), d
   if (tid < 64) {
     stc<kCout>((uint32_t*)(yb + 4) + tid, ((const uint32_t*)s_q)[tid]);
@@ -465,9 +471,12 @@ __device__ __forceinline__ void q8k_block_wave(const Q8KArgs& a, int gb) {
     const h4 hv = {(_Float16)q[0], (_Float16)q[1], (_Float16)q[2], (_Float16)q[3]};
     *(h4*)(a.out_h + off) = hv;
   }
+  if (a.out_8) *(uint32_t*)(a.out_8 + off) = packed;
   int32_t s = (int32_t)q[0] + q[1] + q[2] + q[3];
   s += __shfl_xor(s, 1, 64);
   s += __shfl_xor(s, 2, 64);
+  if (a.bsum_h && (lane & 3) == 0)  // the 16-element group lane / 4 (|s| <= 2032: exact in f16)
+    a.bsum_h[(size_t)row * (a.in_dim >> 4) + (size_t)b * 16 + (lane >> 2)] = __builtin_bit_cast(uint16_t, (_Float16)s);
   const int32_t s_next = __shfl_down(s, 4, 64);  // the next 16-element group
   if ((lane & 7) == 0)
     ((uint32_t*)(yb + 260))[lane >> 3] = (uint32_t)(uint16_t)(int16_t)s | ((uint32_t)(uint16_t)(int16_t)s_next << 16);

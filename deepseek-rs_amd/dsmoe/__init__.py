@@ -29,7 +29,7 @@ EXPORTED = [
     "dsmoe_q8k_quantize", "dsmoe_q8_0_quantize", "dsmoe_gate_up_mid", "dsmoe_down", "dsmoe_moe_sum",
     "dsmoe_q8_0_matvec", "dsmoe_swiglu", "dsmoe_dispatch", "dsmoe_tensor_bytes", "dsmoe_synth_tensor",
     "dsmoe_synth_tensor_host", "dsmoe_stage_name", "dsmoe_set_profiling", "dsmoe_profile_read",
-    "dsmoe_q8k_quantize_h", "dsmoe_gate_up_mid_sorted", "dsmoe_down_sorted", "dsmoe_q8_0_quantize_h",
+    "dsmoe_q8k_quantize_h", "dsmoe_q8k_quantize_i8", "dsmoe_gate_up_mid_sorted", "dsmoe_down_sorted", "dsmoe_q8_0_quantize_h",
     "dsmoe_q8_0_gemm", "dsmoe_q8_0_unpack", "dsmoe_q8_0_gemm_unpacked",
     "dsmoe_gguf_open", "dsmoe_gguf_close", "dsmoe_gguf_tensor_count", "dsmoe_gguf_data_offset", "dsmoe_gguf_tensor_at",
     "dsmoe_gguf_find", "dsmoe_gguf_kv_u32", "dsmoe_gguf_kv_i32_array", "dsmoe_gguf_moe_layer",
@@ -93,7 +93,8 @@ def lib():
         "dsmoe_q8_0_quantize": ([vp, vp, vp, i32, i32, vp], i32),
         "dsmoe_q8k_quantize_h": ([vp, vp, vp, i32, i32, vp], i32),
         "dsmoe_gate_up_mid_sorted": ([vp] * 11 + [i32] * 5 + [f32, vp], i32),
-        "dsmoe_down_sorted": ([vp] * 9 + [i32] * 4 + [vp], i32),
+        "dsmoe_down_sorted": ([vp] * 10 + [i32] * 4 + [vp], i32),
+        "dsmoe_q8k_quantize_i8": ([vp, vp, vp, vp, i32, i32, vp], i32),
         "dsmoe_q8_0_quantize_h": ([vp, vp, vp, vp, i32, i32, vp], i32),
         "dsmoe_q8_0_gemm": ([vp, vp, vp, vp, vp, i32, i32, i32, f32, vp], i32),
         "dsmoe_q8_0_unpack": ([vp, i32, i32, vp, vp, vp], i32),
@@ -240,10 +241,15 @@ def gate_up_mid_sorted(gate, up, xh, xq, sorted_pairs, offsets, tile_offsets, ti
                                          _p(mid_out), d, I, k, E, pairs, clamp, _stream(stream)))
 
 
-def down_sorted(w, mh, mq, sorted_pairs, offsets, tile_offsets, tile_experts, tile_starts, down_out, d, I, E,
-                pairs, stream=None):
-    check(lib().dsmoe_down_sorted(_p(w), _p(mh), _p(mq), _p(sorted_pairs), _p(offsets), _p(tile_offsets),
-                                  _p(tile_experts), _p(tile_starts), _p(down_out), d, I, E, pairs, _stream(stream)))
+def q8k_quantize_i8(x, out, out_i8, bsum_h, in_dim, rows, stream=None):
+    check(lib().dsmoe_q8k_quantize_i8(_p(x), _p(out), _p(out_i8), _p(bsum_h), in_dim, rows, _stream(stream)))
+
+
+def down_sorted(w, m8, bsum_h, mq, sorted_pairs, offsets, tile_offsets, tile_experts, tile_starts, down_out, d, I,
+                E, pairs, stream=None):
+    check(lib().dsmoe_down_sorted(_p(w), _p(m8), _p(bsum_h), _p(mq), _p(sorted_pairs), _p(offsets),
+                                  _p(tile_offsets), _p(tile_experts), _p(tile_starts), _p(down_out), d, I, E, pairs,
+                                  _stream(stream)))
 
 
 def q8_0_quantize_h(x, xq, xscale, out_h, in_dim, rows, stream=None):

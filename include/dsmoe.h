@@ -193,6 +193,14 @@ int dsmoe_q8k_quantize(const float* x, void* out, int32_t in_dim, int32_t rows, 
 int dsmoe_q8k_quantize_h(const float* x, void* out, uint16_t* out_h, int32_t in_dim, int32_t rows,
                          dsmoe_stream_t stream);
 
+/* q8k_quantize as above, also writing the quantized values as int8
+ * [rows][in_dim] (out_i8, 16-byte aligned) and the sum of each 16-element
+ * group as f16 [rows][in_dim/16] (bsum_h; the bsums of the Q8_K block, exact
+ * in f16): the activation operands of the int8 grouped down.  The two
+ * copies have no reference counterpart. */
+int dsmoe_q8k_quantize_i8(const float* x, void* out, int8_t* out_i8, uint16_t* bsum_h, int32_t in_dim, int32_t rows,
+                          dsmoe_stream_t stream);
+
 /* quantize_q8_0 as below, also writing the codes as f16 [rows][in_dim]
  * (out_h; no reference counterpart): the operand of dsmoe_q8_0_gemm. */
 int dsmoe_q8_0_quantize_h(const float* x, int8_t* xq, float* xscale, uint16_t* out_h, int32_t in_dim, int32_t rows,
@@ -255,13 +263,14 @@ int dsmoe_down_em(const void* down, const void* mq, const uint32_t* sorted_pairs
  * (block_m = DSMOE_GROUPED_TILE_M), the per-pair values dsmoe_down computes
  * up to f32 rounding of the order in which a row's superblock values are
  * added (each superblock's integer sums and block value are the
- * reference's); mh/mq: Q8_K(mid) from dsmoe_q8k_quantize_h.  The slot sum is
- * dsmoe_moe_sum.  Matrix cores, exact integer codes in f16; d a multiple of
- * 256. */
-int dsmoe_down_sorted(const void* down, const uint16_t* mh, const void* mq, const uint32_t* sorted_pairs,
-                      const uint32_t* offsets, const uint32_t* tile_offsets, const uint32_t* tile_experts,
-                      const uint32_t* tile_starts, float* down_out, int32_t d, int32_t I, int32_t E, int32_t pairs,
-                      dsmoe_stream_t stream);
+ * reference's); m8/bsum_h/mq: Q8_K(mid) from dsmoe_q8k_quantize_i8.  The
+ * slot sum is dsmoe_moe_sum.  int8 matrix cores (weights sc * q and the mid
+ * codes are exact int8, each superblock's isum an exact int32); d a multiple
+ * of 256. */
+int dsmoe_down_sorted(const void* down, const int8_t* m8, const uint16_t* bsum_h, const void* mq,
+                      const uint32_t* sorted_pairs, const uint32_t* offsets, const uint32_t* tile_offsets,
+                      const uint32_t* tile_experts, const uint32_t* tile_starts, float* down_out, int32_t d, int32_t I,
+                      int32_t E, int32_t pairs, dsmoe_stream_t stream);
 
 /* moe_down_qwarp32 + moe_sum / moe_down_sum6_qwarp32 (engine/src/kernels/
  * moe.rs:821-866, :922-1005): down_out[pair][row] = Q2_K row . Q8_K

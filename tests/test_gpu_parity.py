@@ -319,14 +319,20 @@ def test_gate_up_sorted_matches_per_pair(gpu, d, I, E, T, k, skew, big):
     # down on the same pairs: grouped MFMA vs the per-pair kernel
     dn = dsmoe.synth(dsmoe.FMT_Q2_K, 3, 3, E, d, I, sigma=0.02, device=gpu)
     mq = torch.empty(P_ * (I // 256) * 292, dtype=torch.uint8, device=gpu)
-    mh = torch.empty(P_, I, dtype=torch.int16, device=gpu)
-    dsmoe.q8k_quantize_h(m_ref, mq, mh, I, P_)
+    m8 = torch.empty(P_, I, dtype=torch.int8, device=gpu)
+    bsh = torch.empty(P_, I // 16, dtype=torch.int16, device=gpu)
+    dsmoe.q8k_quantize_i8(m_ref, mq, m8, bsh, I, P_)
     dd_ref = torch.empty(P_, d, device=gpu)
     ro = torch.empty(T, d, device=gpu)
     dsmoe.down(dn, mq, dsel, dd_ref, ro, d, I, T, k, E)
     dd = torch.full((P_, d), float("nan"), device=gpu)
-    dsmoe.down_sorted(dn, mh, mq, sp, offsets, toff, texp, tst, dd, d, I, E, P_)
+    dsmoe.down_sorted(dn, m8, bsh, mq, sp, offsets, toff, texp, tst, dd, d, I, E, P_)
     torch.cuda.synchronize()
+    # the int8 codes and f16 group sums are the Q8_K block's qs and bsums
+    blk = np_(mq).reshape(P_, I // 256, 292)
+    assert np.array_equal(np_(m8).reshape(P_, I), blk[:, :, 4:260].copy().view(np.int8).reshape(P_, I))
+    bs16 = blk[:, :, 260:292].copy().view(np.int16).reshape(P_, I // 16)
+    assert np.array_equal(np_(bsh).view(np.float16).astype(np.float32), bs16.astype(np.float32))
     got, want = np_(dd).astype(np.float64), np_(dd_ref).astype(np.float64)
     assert np.isfinite(got).all()
     r = rel_l2(got, want)
