@@ -411,31 +411,38 @@ def main():
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / args.steps
 
-    # the same steps replayed from HIP graphs (one captured call per weight set
-    # and activation slot; dsmoe_forward allocates nothing and sets no memory)
+    # the same steps replayed from HIP graphs.  A graph holds kGraphSteps
+    # consecutive layer calls (rotating weights and activations, as a
+    # captured decode step over a stack of layers would): each graph launch
+    # costs the GPU a fixed idle gap (about 8 us between the end of one
+    # replay and the start of the next, measured with a kernel trace; no gap
+    # appears between the kernel nodes inside a replay), which one call per
+    # graph would pay per layer.
     graph_ms = None
+    kGraphSteps = 64
     if T <= 8 and not args.no_graph:
-        graphs = []
         cs = torch.cuda.Stream()
         cs.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(cs):
             step(0)
         torch.cuda.current_stream().wait_stream(cs)
-        nslots = L * 4
-        for i in range(nslots):
+        graphs = []
+        for gi in range(2):
             gr = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gr):
-                step(i)
+                for i in range(kGraphSteps):
+                    step(gi * kGraphSteps + i)
             graphs.append(gr)
-        for i in range(args.warmup):
-            graphs[i % nslots].replay()
+        reps = max(1, args.steps // kGraphSteps)
+        for i in range(2):
+            graphs[i % 2].replay()
         torch.cuda.synchronize()
         start.record()
-        for i in range(args.steps):
-            graphs[i % nslots].replay()
+        for i in range(reps):
+            graphs[i % 2].replay()
         stop.record()
         torch.cuda.synchronize()
-        graph_ms = start.elapsed_time(stop) / args.steps
+        graph_ms = start.elapsed_time(stop) / (reps * kGraphSteps)
         del graphs
 
     # per-stage timing pass (events around each stage on the launch stream)
@@ -539,7 +546,10 @@ def main():
         "stages": stage_rows,
         "graph_replay": None if graph_ms is None else {
             "ms_per_step": round(graph_ms, 5), "tokens_per_s": round(T / (graph_ms * 1e-3), 1),
-            "note": "the same steps captured as HIP graphs (one per weight set and activation slot) and replayed"},
+            "steps_per_graph": kGraphSteps,
+            "note": f"the same layer calls captured {kGraphSteps} to a HIP graph (rotating weight sets and "
+                    f"activations) and replayed; one graph launch costs an ~8 us idle gap on the GPU, so a graph "
+                    f"per layer call would be slower than eager launches"},
         "prefill": prefill.get("c5"),
         "prefill_variants": {n: v for n, v in prefill.items() if n != "c5"},
         "other_configs": others,
