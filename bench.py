@@ -22,6 +22,11 @@ sys.path.insert(0, os.path.join(ROOT, "deepseek-rs_amd"))
 
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0  # dense f16 MFMA, MI355X
+MFMA_I8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
+# the matrix-core type each grouped kernel's main product runs on (dn_grouped
+# multiplies exact int8 weight and activation codes; the others f16)
+STAGE_MFMA = {"gu_grouped": ("f16", MFMA_PEAK_TFLOPS), "dn_grouped": ("int8", MFMA_I8_PEAK_TOPS),
+              "shared_up": ("f16", MFMA_PEAK_TFLOPS), "shared_dn": ("f16", MFMA_PEAK_TFLOPS)}
 
 
 def prefill_flops(cfg, T):
@@ -78,6 +83,8 @@ def prefill_bench(case, steps, warmup, dev):
         if fl.get(name):
             row["flops"] = int(fl[name])
             row["TFLOPs"] = round(fl[name] / (avg * 1e-3) / 1e12, 1)
+            typ, peak = STAGE_MFMA[name]
+            row["mfma_type"], row["frac_of_type_peak"] = typ, round(row["TFLOPs"] / peak, 4)
         rows[name] = row
     dom = max((n for n in rows if "flops" in rows[n]), key=lambda n: rows[n]["avg_us"])
     tot_fl = sum(fl.values())
@@ -94,7 +101,10 @@ def prefill_bench(case, steps, warmup, dev):
         "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_step": round(ms, 4), "steps": steps,
         "mfma_flops_per_step": int(tot_fl), "achieved_TFLOPs": round(tot_fl / (ms * 1e-3) / 1e12, 1),
         "frac_of_mfma_peak": round(tot_fl / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
-        "mfma_dtype": "f16 (exact small-integer operands, f32 accumulation)",
+        "mfma_dtype": "f16 (exact small-integer operands, f32 accumulation) for gate/up and the shared expert; "
+                      "int8 (exact, i32 accumulation) for the routed down projection; frac_of_mfma_peak and each "
+                      "stage's TFLOPs count 2 flops per multiply-add against the f16 peak, frac_of_type_peak "
+                      "against the peak of the type the stage runs on",
         "roofline": {"bound": "mfma", "kernel": PREFILL_KERNEL[dom], "achieved": rows[dom]["TFLOPs"],
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(rows[dom]["TFLOPs"] / MFMA_PEAK_TFLOPS, 4),

@@ -10,9 +10,8 @@ design notes quote).  Reads only CSV files that rocprofv3 wrote (run it with
       256 MiB device copy: 256 MiB read and 256 MiB written)
   python deepseek-rs_amd/profile_summary.py counters OUT DIR [DIR ...] --title T --cmd C
       medians per kernel and counter over the dispatches in DIR/*_counter_collection.csv;
-      with SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE in one run also
-      mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDS * GRBM_GUI_ACTIVE / XCDS),
-      the fraction of the dispatch's time the matrix cores were busy
+      plus the busy fractions derived() forms from the counters of one run
+      (VALU, LDS, LDS bank conflicts, matrix cores, TA stalled by the L1)
 
 Every table row of a dsmoe kernel carries the hash of the code object it was
 measured on (`code_object=`), so a summary of an older build is recognisable
@@ -31,7 +30,7 @@ GEMM_PREFIXES = ("dsmoe_gu_grouped", "dsmoe_dn_grouped", "dsmoe_q80_gemm", "dsmo
                  "dsmoe_probe")
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 COPY_KIB = 256 * 1024  # the calibration copy: 256 MiB read and 256 MiB written
-SIMDS, XCDS = 1024, 8  # MI355X: 256 compute units x 4 SIMDs; GRBM_GUI_ACTIVE is summed over the 8 XCDs
+SIMDS, XCDS, CUS = 1024, 8, 256  # MI355X: 256 compute units x 4 SIMDs; GRBM_GUI_ACTIVE is summed over the 8 XCDs
 
 
 def code_object_hash(kernel, lib_dir=None):
@@ -109,6 +108,36 @@ def traffic(out, fetch_dir, write_dir, config, path, title, cmd):
     open(out, "w").write("\n".join(lines) + "\n")
 
 
+def derived(med):
+    """Busy fractions from one run's medians (rocprofv3's derived-metric
+    formulas; GRBM_GUI_ACTIVE is summed over the XCDs in these CSVs, so its
+    per-XCD value, the kernel's cycles, is the sum / XCDS):
+      valu_busy  = SQ_ACTIVE_INST_VALU / (CUS * cycles)      (rocprofv3 VALUBusy / 100)
+      lds_busy   = SQ_ACTIVE_INST_LDS / (CUS * cycles)       (the same formula for the LDS)
+      lds_bank_conflict = SQ_LDS_BANK_CONFLICT / (CUS * cycles)  (rocprofv3 LDSBankConflict / 100)
+      mfma_busy  = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDS * cycles)
+      mfma_coexec = SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES (MFMA time with VALU issuing beside it)
+      ta_stalled_by_tc = TA_ADDR_STALLED_BY_TC_CYCLES / TA_TA_BUSY (share of the address unit's busy time
+                   spent waiting for the L1)"""
+    out = {}
+    g = med.get("GRBM_GUI_ACTIVE")
+    if g:
+        cyc = g / XCDS
+        if "SQ_ACTIVE_INST_VALU" in med:
+            out["valu_busy"] = med["SQ_ACTIVE_INST_VALU"] / (CUS * cyc)
+        if "SQ_ACTIVE_INST_LDS" in med:
+            out["lds_busy"] = med["SQ_ACTIVE_INST_LDS"] / (CUS * cyc)
+        if "SQ_LDS_BANK_CONFLICT" in med:
+            out["lds_bank_conflict"] = med["SQ_LDS_BANK_CONFLICT"] / (CUS * cyc)
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in med:
+            out["mfma_busy"] = med["SQ_VALU_MFMA_BUSY_CYCLES"] / (SIMDS * cyc)
+    if med.get("SQ_VALU_MFMA_BUSY_CYCLES") and "SQ_VALU_MFMA_COEXEC_CYCLES" in med:
+        out["mfma_coexec"] = med["SQ_VALU_MFMA_COEXEC_CYCLES"] / med["SQ_VALU_MFMA_BUSY_CYCLES"]
+    if med.get("TA_TA_BUSY") and "TA_ADDR_STALLED_BY_TC_CYCLES" in med:
+        out["ta_stalled_by_tc"] = med["TA_ADDR_STALLED_BY_TC_CYCLES"] / med["TA_TA_BUSY"]
+    return out
+
+
 def counters(out, dirs, title, cmd):
     lines = _header(title, cmd)
     lines.append("# medians over the dispatches of each kernel; counters summed over their hardware instances")
@@ -118,8 +147,7 @@ def counters(out, dirs, title, cmd):
                 continue
             med = {c: statistics.median(v) for c, v in cs.items()}
             vals = "  ".join(f"{c}={m:.4g}" for c, m in sorted(med.items()))
-            if med.get("GRBM_GUI_ACTIVE") and "SQ_VALU_MFMA_BUSY_CYCLES" in med:
-                vals += f"  mfma_busy={med['SQ_VALU_MFMA_BUSY_CYCLES'] / (SIMDS * med['GRBM_GUI_ACTIVE'] / XCDS):.3f}"
+            vals += "".join(f"  {n}={v:.3f}" for n, v in derived(med).items())
             lines.append(f"{k}  code_object={code_object_hash(k) or '-'}  {vals}")
     open(out, "w").write("\n".join(lines) + "\n")
 

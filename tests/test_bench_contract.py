@@ -73,3 +73,22 @@ def test_cpu_baseline_value_is_the_all_core_run():
     pair = b.cpu_pair(case, hw, xs, 0.1, None, None)
     assert pair["threads"] == os.cpu_count() and pair["tokens_per_s_1_thread"] > 0
     assert np.isfinite(pair["tokens_per_s"])
+
+
+def test_profile_summary_busy_fractions():
+    """derived() turns one run's counter medians into busy fractions:
+    a kernel whose 256 CUs each issue VALU work on every one of its cycles
+    (GRBM_GUI_ACTIVE summed over 8 XCDs) is valu_busy 1.0; the matrix-core
+    share is per SIMD (1024 of them); the TA share is a plain ratio."""
+    sys.path.insert(0, os.path.join(ROOT, "deepseek-rs_amd"))
+    import profile_summary as P
+    cyc = 1000.0
+    d = P.derived({"GRBM_GUI_ACTIVE": 8 * cyc, "SQ_ACTIVE_INST_VALU": 256 * cyc, "SQ_ACTIVE_INST_LDS": 64 * cyc,
+                   "SQ_LDS_BANK_CONFLICT": 128 * cyc, "SQ_VALU_MFMA_BUSY_CYCLES": 512 * cyc,
+                   "SQ_VALU_MFMA_COEXEC_CYCLES": 128 * cyc, "TA_TA_BUSY": 400.0,
+                   "TA_ADDR_STALLED_BY_TC_CYCLES": 100.0})
+    assert d == {"valu_busy": 1.0, "lds_busy": 0.25, "lds_bank_conflict": 0.5, "mfma_busy": 0.5,
+                 "mfma_coexec": 0.25, "ta_stalled_by_tc": 0.25}
+    # without the clock only the ratios that need none are formed
+    assert P.derived({"SQ_ACTIVE_INST_VALU": 1.0, "TA_TA_BUSY": 2.0, "TA_ADDR_STALLED_BY_TC_CYCLES": 1.0}) == \
+        {"ta_stalled_by_tc": 0.5}
