@@ -395,6 +395,8 @@ def main():
     L = max(1, args.layers)
     print(f"[bench] config={case.name} T={T} layers={L}: generating weights", file=sys.stderr, flush=True)
     layers = [C.make_weights(case, layer=i, device=dev) for i in range(L)]
+    if T > 8:  # batches: the shared expert unpacked once per weight load, as an engine would
+        layers = [w.unpack_shared(cfg) for w in layers]
     xs = [C.make_x(case, T=T, step=s, device=dev) for s in range(16)]
     layer = dsmoe.MoeLayer(cfg, T)
     path = "staged"
@@ -506,6 +508,8 @@ def main():
             else:  # decode-sized configs rotate over enough copies to exceed the 256 MB last-level cache
                 nl = max(1, -(-(512 << 20) // layer_bytes(oc.cfg, oc.cfg.n_expert))) if oc.T <= 8 else 1
                 ow = [C.make_weights(oc, layer=i, device=dev) for i in range(nl)]
+                if oc.T > 8:
+                    ow = [w.unpack_shared(oc.cfg) for w in ow]
             others[name] = config_bench(oc, ow, 50 if oc.T <= 8 else 20, 5, dev)
             del ow
 

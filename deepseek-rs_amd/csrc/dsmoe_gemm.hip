@@ -278,8 +278,9 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
 
   // one superblock from LDS buffer buf and raw rows gr / ur (kEven: the qs
   // start 2 bytes into the loaded words)
-  auto superblock = [&](auto even_tag, uint32_t* gr, uint32_t* ur) {
+  auto superblock = [&](auto even_tag, auto two_tag, uint32_t* gr, uint32_t* ur) {
     constexpr bool kEven = decltype(even_tag)::value;  // even superblocks use buffer 0
+    constexpr bool kTwo = decltype(two_tag)::value;    // pairs 32-63 live (else their products are skipped)
     auto& sA = kEven ? sA0 : sA1;
     auto& s_yd = kEven ? s_yd0 : s_yd1;
     // the block scale, then the qs words realigned in place (even superblocks
@@ -326,11 +327,13 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
       const half8 bu = __builtin_bit_cast(half8, u32x4{mul(uv.x, um.x), mul(uv.y, um.y), mul(uv.z, um.z), mul(uv.w, um.w)});
       const int c = lk ^ (2 * ks);
       const half8 a0 = __builtin_bit_cast(half8, sA[rowa + c]);
-      const half8 a1 = __builtin_bit_cast(half8, sA[rowa + 32 * 32 + c]);
       ag0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bg, ag0, 0, 0, 0);
       au0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bu, au0, 0, 0, 0);
-      ag1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bg, ag1, 0, 0, 0);
-      au1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bu, au1, 0, 0, 0);
+      if constexpr (kTwo) {
+        const half8 a1 = __builtin_bit_cast(half8, sA[rowa + 32 * 32 + c]);
+        ag1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bg, ag1, 0, 0, 0);
+        au1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bu, au1, 0, 0, 0);
+      }
     }
     // block values 0.125 * xd * yd * sum (quantize.rs:763-812), added in superblock order
     const float cg = 0.125f * f16_to_f32_ftz((uint16_t)dg);
@@ -339,34 +342,42 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
 #pragma unroll
     for (int k = 0; k < 16; k++) {
       const int m = 8 * (k >> 2) + 4 * kh + (k & 3);
-      const float y0 = yd[m], y1 = yd[32 + m];
+      const float y0 = yd[m];
       rg0[k] = __builtin_fmaf(cg * y0, ag0[k], rg0[k]);
       ru0[k] = __builtin_fmaf(cu * y0, au0[k], ru0[k]);
-      rg1[k] = __builtin_fmaf(cg * y1, ag1[k], rg1[k]);
-      ru1[k] = __builtin_fmaf(cu * y1, au1[k], ru1[k]);
+      if constexpr (kTwo) {
+        const float y1 = yd[32 + m];
+        rg1[k] = __builtin_fmaf(cg * y1, ag1[k], rg1[k]);
+        ru1[k] = __builtin_fmaf(cu * y1, au1[k], ru1[k]);
+      }
     }
   };
 
-  uint32_t gE[17], uE[17], gO[17], uO[17];
-  load17(raw_at(grow, 0), gE);
-  load17(raw_at(urow, 0), uE);
-  issue_a(0, std::false_type{});
-  for (int b = 0; b < nb; b += 2) {  // nb is even (d is a multiple of 512)
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    issue_a(b + 1, std::true_type{});
-    load17(raw_at(grow, b + 1), gO);
-    load17(raw_at(urow, b + 1), uO);
-    superblock(std::true_type{}, gE, uE);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (b + 2 < nb) {
-      issue_a(b + 2, std::false_type{});
-      load17(raw_at(grow, b + 2), gE);
-      load17(raw_at(urow, b + 2), uE);
+  // A tile of at most 32 pairs (the partial last tile of an expert) skips
+  // the products and block values of pairs 32-63: its own copy of the loop
+  auto main_loop = [&](auto two_tag) {
+    uint32_t gE[17], uE[17], gO[17], uO[17];
+    load17(raw_at(grow, 0), gE);
+    load17(raw_at(urow, 0), uE);
+    issue_a(0, std::false_type{});
+    for (int b = 0; b < nb; b += 2) {  // nb is even (d is a multiple of 512)
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      issue_a(b + 1, std::true_type{});
+      load17(raw_at(grow, b + 1), gO);
+      load17(raw_at(urow, b + 1), uO);
+      superblock(std::true_type{}, two_tag, gE, uE);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (b + 2 < nb) {
+        issue_a(b + 2, std::false_type{});
+        load17(raw_at(grow, b + 2), gE);
+        load17(raw_at(urow, b + 2), uE);
+      }
+      superblock(std::false_type{}, two_tag, gO, uO);
     }
-    superblock(std::false_type{}, gO, uO);
-  }
+  };
+  if (cnt > 32) main_loop(std::true_type{}); else main_loop(std::false_type{});
 
   // SwiGLU (utils.rs:141-163) and the routing weight; rows of dead pairs are not stored
 #pragma unroll
@@ -505,8 +516,9 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) run[q][i] = 0.0f;
 
-  auto superblock = [&](auto buf_tag, const uint32_t* r) {
+  auto superblock = [&](auto buf_tag, auto two_tag, const uint32_t* r) {
     constexpr bool B1 = decltype(buf_tag)::value;
+    constexpr bool kTwo = decltype(two_tag)::value;  // pairs 32-63 live (else their products are skipped)
     auto& sA = B1 ? sA1 : sA0;
     auto& sBS = B1 ? sBS1 : sBS0;
     auto& s_yd = B1 ? s_yd1 : s_yd0;
@@ -534,9 +546,11 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; i++) bv[i] = (int)__builtin_amdgcn_perm(tab, tab, (q[i] >> sh) & 0x03030303u);
       const int4v a0 = __builtin_bit_cast(int4v, pa[2 * s]);
-      const int4v a1 = __builtin_bit_cast(int4v, pa[32 * kDnRowSlots + 2 * s]);
       acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bv, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bv, acc[1], 0, 0, 0);
+      if constexpr (kTwo) {
+        const int4v a1 = __builtin_bit_cast(int4v, pa[32 * kDnRowSlots + 2 * s]);
+        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bv, acc[1], 0, 0, 0);
+      }
     }
     // summs = bsums . min over the 16 groups: one K = 16 product per tile
     // (bsums |.| <= 16 * 127 and the 4-bit mins are exact in f16)
@@ -554,7 +568,8 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) z[i] = 0.0f;
     sm[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, sBS[64 * kh + l32]), mn, z, 0, 0, 0);
-    sm[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, sBS[64 * kh + 32 + l32]), mn, z, 0, 0, 0);
+    if constexpr (kTwo)
+      sm[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, sBS[64 * kh + 32 + l32]), mn, z, 0, 0, 0);
     // block value yd * (d * isum - dmin * summs) (the reference's
     // dall * isum - dmin' * summs with yd factored out)
     const float dn0 = f16_to_f32_ftz_nb((uint16_t)(r[12] & 0xFFFF)), ndm = -f16_to_f32_ftz_nb((uint16_t)(r[12] >> 16));
@@ -563,33 +578,39 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
     for (int k = 0; k < 16; k++) {
       const int m = 8 * (k >> 2) + 4 * kh + (k & 3);
       run[0][k] = __builtin_fmaf(yd[m], __builtin_fmaf(ndm, sm[0][k], dn0 * (float)acc[0][k]), run[0][k]);
-      run[1][k] = __builtin_fmaf(yd[32 + m], __builtin_fmaf(ndm, sm[1][k], dn0 * (float)acc[1][k]), run[1][k]);
+      if constexpr (kTwo)
+        run[1][k] = __builtin_fmaf(yd[32 + m], __builtin_fmaf(ndm, sm[1][k], dn0 * (float)acc[1][k]), run[1][k]);
     }
   };
 
-  uint32_t e0[13], o0[13];
-  load_q2_i8(row0, kh, e0);
-  const std::false_type buf0{};
-  const std::true_type buf1{};
-  issue_a(0, buf0);
-  for (int b = 0; b < nb; b += 2) {
-    const bool odd = b + 1 < nb;  // the odd superblock of this pair exists
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (odd) {
-      issue_a(b + 1, buf1);
-      load_q2_i8(row0 + (size_t)(b + 1) * Q2K_BYTES, kh, o0);
+  // A tile of at most 32 pairs (the partial last tile of an expert) skips
+  // the products and block values of pairs 32-63: its own copy of the loop
+  auto main_loop = [&](auto two_tag) {
+    uint32_t e0[13], o0[13];
+    load_q2_i8(row0, kh, e0);
+    const std::false_type buf0{};
+    const std::true_type buf1{};
+    issue_a(0, buf0);
+    for (int b = 0; b < nb; b += 2) {
+      const bool odd = b + 1 < nb;  // the odd superblock of this pair exists
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (odd) {
+        issue_a(b + 1, buf1);
+        load_q2_i8(row0 + (size_t)(b + 1) * Q2K_BYTES, kh, o0);
+      }
+      superblock(buf0, two_tag, e0);
+      if (!odd) break;
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (b + 2 < nb) {
+        issue_a(b + 2, buf0);
+        load_q2_i8(row0 + (size_t)(b + 2) * Q2K_BYTES, kh, e0);
+      }
+      superblock(buf1, two_tag, o0);
     }
-    superblock(buf0, e0);
-    if (!odd) break;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (b + 2 < nb) {
-      issue_a(b + 2, buf0);
-      load_q2_i8(row0 + (size_t)(b + 2) * Q2K_BYTES, kh, e0);
-    }
-    superblock(buf1, o0);
-  }
+  };
+  if (cnt > 32) main_loop(std::true_type{}); else main_loop(std::false_type{});
 
 #pragma unroll
   for (int q = 0; q < 2; q++)
