@@ -186,22 +186,12 @@ constexpr int kMinWgs = 512;
 constexpr int kDecodeMaxT = kMaxDecodeT;  // row-streaming (matvec) launches up to 8 tokens, batch paths above
 constexpr int kEmMaxLoad = 4;    // pairs per expert (on average) up to which batches run expert-major
 constexpr int kQ80MaxSplit = 8;  // class groups of a split shared-expert GEMM (up to 256 tokens)
-#ifdef DSM_PROBE
-// measurement builds only: launch-shape overrides from the environment
-int dsm_tune(const char* name, int def) {
-  const char* v = getenv(name);
-  return v ? atoi(v) : def;
-}
-#define DSM_TUNE(name, def) dsm_tune(name, def)
-#else
-#define DSM_TUNE(name, def) (def)
-#endif
 // Pairs per expert-major chunk: a chunk keeps its activations in LDS, so a
 // smaller chunk leaves room for more workgroups per compute unit, a larger
 // one streams a busy expert's rows fewer times.  4 measured best on c3
 // (T = 32, about 1.5 pairs per used expert) and c4 (T = 128, about 4)
 // against 1, 2 and 8.
-int em_pairs() { return DSM_TUNE("DSM_EM_NP", 4); }
+int em_pairs() { return 4; }
 
 int pow2_floor(int v) {
   int p = 1;
@@ -326,7 +316,7 @@ static int prep_impl(const RouterLogitsArgs* r, const Q8KArgs* q8k, const Q80Arg
     // per layer, at 256 (c4, T = 128, where the concurrent shared expert is
     // the longer chain) ~0.6 % slower
     const unsigned big = (unsigned)(((r->E + 7) / 8) * ((r->T + 15) / 16));
-    if (big < (unsigned)DSM_TUNE("DSM_ROUTER_SMALL_BELOW", 128))
+    if (big < 128u)
       DSM_TRY(launch(K_ROUTER_TILE_S, dim3(((r->E + 3) / 4) * ((r->T + 7) / 8)), dim3(256), 0, stream, *r));
     else
       DSM_TRY(launch(K_ROUTER_TILE, dim3(big), dim3(256), 0, stream, *r));
@@ -766,7 +756,7 @@ int dsmoe_q8_0_gemm(const void* w0, const void* w1, const uint16_t* xh, const fl
 // Batches of at least q80_wide_min_t() tokens take it: below that the grid of
 // 128-token tiles is too small to fill the chip and the split exact kernel
 // is faster.
-static int q80_wide_min_t() { return DSM_TUNE("DSM_Q80_WIDE_MIN_T", 1024); }
+static int q80_wide_min_t() { return 1024; }
 static bool q80_wide_fits(int d, int Is) {
   return d % 128 == 0 && Is % 64 == 0 && d <= 8192 && Is <= 8192;
 }
@@ -1117,7 +1107,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // Few pairs per expert (at most kEmMaxLoad on average): the routed experts
   // stream their weights once per chunk of em_pairs() pairs
   // (expert-major matvec) instead of dequantizing them into MFMA tiles.
-  const bool em = grouped && (int64_t)P <= (int64_t)DSM_TUNE("DSM_EM_MAX_LOAD", kEmMaxLoad) * E && em_fits(cf);
+  const bool em = grouped && (int64_t)P <= (int64_t)kEmMaxLoad * E && em_fits(cf);
   // Large batches run the shared expert through the unpacked wide GEMM, over
   // the caller's unpacked matrices when the weights carry them (all six
   // pointers), else over the context's copies unpacked in this call.
@@ -1132,12 +1122,12 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // expert); with
   // stage profiling on, every stage runs on the caller's stream so each
   // stage's time is its own
-  const bool fork = grouped && cf.shared_fmt == 0 && c->side && !c->profiling && DSM_TUNE("DSM_SIDE_SHARED", 1);
+  const bool fork = grouped && cf.shared_fmt == 0 && c->side && !c->profiling;
   hipStream_t shs = fork ? c->side : (hipStream_t)stream;
   // In the row-streaming path the selection needs no launch of its own:
   // every routed gate/up workgroup runs it for its token.
   const bool up_rows = !grouped && up_rows_fits(d) && (cf.shared_fmt != 0 || q80_rows_fits(d));
-  const bool fuse_sel = up_rows && !c->hash && DSM_TUNE("DSM_FUSE_SEL", 1);
+  const bool fuse_sel = up_rows && !c->hash;
   if (fork) {
     if (hipEventRecord(c->ev_fork, (hipStream_t)stream) != hipSuccess ||
         hipStreamWaitEvent(c->side, c->ev_fork, 0) != hipSuccess)
