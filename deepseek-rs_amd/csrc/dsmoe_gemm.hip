@@ -4,18 +4,22 @@
 //
 // Pairs (token, slot) are sorted by expert (dsmoe_dispatch) and cut into
 // tiles of up to kGuBM pairs of one expert; a workgroup multiplies one tile
-// by a slab of one expert's weight rows on the matrix cores.  The weights
-// are dequantized per 256-element superblock into LDS as exact small
-// integers in f16, the activations are the Q8_K integers in f16, and
-// v_mfma_f32_32x32x16_f16 accumulates their products in f32.
+// by a slab of one expert's weight rows on the matrix cores.  Gate/up: each
+// lane dequantizes its IQ2_XXS weight row straight into the f16 MFMA operand
+// as exact small integers, the activations are the Q8_K integers in f16, and
+// v_mfma_f32_32x32x16_f16 accumulates their products in f32.  Down: the Q2_K
+// weights sc * q and the mid's Q8_K codes are exact int8 and
+// v_mfma_i32_32x32x32_i8 accumulates in int32.
 //
-// Exactness: every product is an integer of at most 24 bits and every
-// partial sum of one superblock stays an integer below 2^24 (checked per
-// superblock, below), so the f32 accumulator holds the reference's integer
-// block sum exactly, in any summation order.  The per-superblock float
-// epilogue and the sum over superblocks then follow the reference's order
-// (lane-strided partials over 8 lanes, xor butterfly 4, 2, 1: moe.rs:35-41,
-// :622-715), so results are bit-identical to the per-pair kernels.
+// Exactness: every product is an integer below 2^18.  The int32 sums of the
+// down are exact.  A gate/up superblock sum is exact in f32 while its
+// partial sums stay below 2^24 (127 * sum|w| < 2^24 for the row; real weight
+// rows stay far below it); past that, f32 rounds the partial sums, an error
+// of the order of the reference's own f32 epilogue.  The block value of each
+// superblock is formed as in the reference; a row's superblocks are added in
+// order 0, 1, 2, ... where the reference adds per-lane partials and a
+// butterfly (moe.rs:35-41, :622-715), so the results agree with the per-pair
+// kernels to f32 rounding of that order.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -38,7 +42,6 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // Word 3 of a raw buffer descriptor on gfx9 (32-bit data format, no swizzle).
 constexpr int kBufDword3 = 0x00020000;
 constexpr int kRowH = 264;  // f16 per LDS operand row: 256 + 8 (528 B, 132 dwords = 4 mod 32 banks)
-constexpr float kExactBound = 16777216.0f;  // 2^24
 
 // Superblock visiting order: the reference's lane classes l = b mod 8 in the
 // order its butterfly combines them, ((0+4)+(2+6)) + ((1+5)+(3+7)).

@@ -310,6 +310,11 @@ def test_gate_up_sorted_matches_per_pair(gpu, d, I, E, T, k, skew, big):
     q_h = O.q8k_quantize(np_(x), d, T).reshape(T, d // 256, 292)[:, :, 4:260].view(np.int8).reshape(T, d)
     assert np.array_equal(xh_h, q_h.astype(np.float32))
     say(f"  tiles={int(np_(toff)[-1])} max_count={int(np_(counts).max())}")
+    # tiles of at most 32 pairs run their own loop copy (no products for pairs 32-63)
+    fills = [min(64, int(c) - 64 * i) for c in np_(counts) for i in range((int(c) + 63) // 64)]
+    say(f"  tiles with <= 32 pairs: {sum(f <= 32 for f in fills)}, with more: {sum(f > 32 for f in fills)}")
+    if skew and not big:
+        assert any(f <= 32 for f in fills) and any(f > 32 for f in fills)
     got, want = np_(m).astype(np.float64), np_(m_ref).astype(np.float64)
     assert np.isfinite(got).all()
     r = rel_l2(got, want)
