@@ -185,6 +185,7 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 constexpr int kMinWgs = 512;
 constexpr int kDecodeMaxT = kMaxDecodeT;  // row-streaming (matvec) launches up to 8 tokens, batch paths above
 constexpr int kEmMaxLoad = 4;    // pairs per expert (on average) up to which batches run expert-major
+constexpr int kEmDnMaxLoad = 2;  // ... and up to which the down does too (above: the int8 grouped down)
 constexpr int kQ80MaxSplit = 8;  // class groups of a split shared-expert GEMM (up to 256 tokens)
 // Pairs per expert-major chunk: a chunk keeps its activations in LDS, so a
 // smaller chunk leaves room for more workgroups per compute unit, a larger
@@ -854,6 +855,11 @@ struct dsmoe_ctx {
   uint32_t* g_tile_offsets = nullptr;
   uint32_t* g_tile_experts = nullptr;
   uint32_t* g_tile_starts = nullptr;
+  // tiles of kGuBM pairs for the grouped down when the gate/up runs
+  // expert-major (its tiles above are em_pairs() pairs)
+  uint32_t* g_tile_offsets64 = nullptr;
+  uint32_t* g_tile_experts64 = nullptr;
+  uint32_t* g_tile_starts64 = nullptr;
   float* q80_part = nullptr;     // split shared-expert GEMM partials, [kQ80MaxSplit][min(T, 256)][cols]
   uint16_t* shw_h[3] = {};       // shared gate / up / down unpacked for dsmoe_q80_wide (codes as f16)
   // Batches on the wide shared-expert path run the quantization of x and the
@@ -1040,6 +1046,10 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
     A(&c->g_tile_offsets, (E + 1) * 4);
     A(&c->g_tile_experts, max_tiles * 4);
     A(&c->g_tile_starts, max_tiles * 4);
+    const size_t max_tiles64 = P / kGuBM + std::min(E, P);
+    A(&c->g_tile_offsets64, (E + 1) * 4);
+    A(&c->g_tile_experts64, max_tiles64 * 4);
+    A(&c->g_tile_starts64, max_tiles64 * 4);
     A(&c->q80_part, (size_t)kQ80MaxSplit * std::min<size_t>(T, 256) * std::max<size_t>(2 * Is, d) * 4);
     if (cfg->shared_fmt == 0 && q80_wide_fits((int)d, cfg->d_ff_shared) && max_tokens >= q80_wide_min_t()) {
       const size_t is = (size_t)cfg->d_ff_shared;
@@ -1108,6 +1118,10 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // stream their weights once per chunk of em_pairs() pairs
   // (expert-major matvec) instead of dequantizing them into MFMA tiles.
   const bool em = grouped && (int64_t)P <= (int64_t)kEmMaxLoad * E && em_fits(cf);
+  // The int8 grouped down overtakes the expert-major one from about 2 pairs
+  // per expert (c4, 4 per expert: 386 against 526 us), well before the
+  // gate/up does.
+  const bool em_dn = em && (int64_t)P <= (int64_t)kEmDnMaxLoad * E;
   // Large batches run the shared expert through the unpacked wide GEMM, over
   // the caller's unpacked matrices when the weights carry them (all six
   // pointers), else over the context's copies unpacked in this call.
@@ -1159,6 +1173,9 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     if (grouped)  // moe_count/prefix/scatter_sorted_pairs + tiles (moe.rs:299-362, 547-596)
       DSM_TRY(dsmoe_dispatch(sel, P, E, em ? em_pairs() : kGuBM, c->g_counts, c->g_offsets, c->g_sorted,
                              c->g_tile_offsets, c->g_tile_experts, c->g_tile_starts, stream));
+    if (em && !em_dn)  // the same sort again, cut into the grouped down's tiles
+      DSM_TRY(dsmoe_dispatch(sel, P, E, kGuBM, c->g_counts, c->g_offsets, c->g_sorted, c->g_tile_offsets64,
+                             c->g_tile_experts64, c->g_tile_starts64, stream));
   }
   // 3. routed + shared gate/up/SwiGLU              (session.rs:1910-1959, 2075-2112)
   // The row-streaming launch also quantizes the mid rows (step 4) when the
@@ -1239,7 +1256,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // 4. Q8_K(mid) + Q8_0 / Q8_K of the shared mid  (session.rs:1964-1976, 2114-2127)
   if (!fuse_midq) {
     StageScope sc(c, DSMOE_STAGE_MIDQ, stream);
-    Q8KArgs qa{c->mid, c->midq, I, P, nullptr, grouped && !em ? c->m8 : nullptr, grouped && !em ? c->bsh : nullptr};
+    Q8KArgs qa{c->mid, c->midq, I, P, nullptr, grouped && !em_dn ? c->m8 : nullptr, grouped && !em_dn ? c->bsh : nullptr};
     Q8KArgs qb{c->sh_mid, c->sh_midq, Is, T};
     Q80Args q80{c->sh_mid, c->sh_q80, c->sh_s80, Is, T, grouped ? c->shh : nullptr};
     if (fork) {  // the shared mid is quantized on the side stream
@@ -1262,12 +1279,14 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     if (grouped) {
       {
         StageScope sg(c, DSMOE_STAGE_DN_GROUPED, stream);
-        if (em) {
+        if (em_dn) {
           DSM_TRY(dsmoe_down_em(w->down, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets, c->g_tile_experts,
                                 c->g_tile_starts, c->down_out, d, I, E, P, em_pairs(), stream));
         } else {
-          DSM_TRY(dsmoe_down_sorted(w->down, c->m8, c->bsh, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets,
-                                    c->g_tile_experts, c->g_tile_starts, c->down_out, d, I, E, P, stream));
+          DSM_TRY(dsmoe_down_sorted(w->down, c->m8, c->bsh, c->midq, c->g_sorted, c->g_offsets,
+                                    em ? c->g_tile_offsets64 : c->g_tile_offsets,
+                                    em ? c->g_tile_experts64 : c->g_tile_experts,
+                                    em ? c->g_tile_starts64 : c->g_tile_starts, c->down_out, d, I, E, P, stream));
         }
       }
       DSM_TRY(dsmoe_moe_sum(c->down_out, routed_out, d, K, T, stream));
