@@ -1098,14 +1098,15 @@ size_t dsmoe_scratch_bytes(const dsmoe_ctx* c) { return c ? c->bytes : 0; }
 
 static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, int32_t T, float* shared_out,
                   float* routed_out, int32_t* selected, float* weights, dsmoe_stream_t stream) {
-  if (!c || !w || !x || !routed_out) return fail(DSMOE_ERR_INVALID, "forward: null pointer");
+  if (!c || !w) return fail(DSMOE_ERR_INVALID, "forward: null pointer");
   if (T < 0 || T > c->max_tokens) return fail(DSMOE_ERR_INVALID, "forward: T outside 0..max_tokens");
+  if (T == 0) return DSMOE_OK;  // no token: nothing is read or written (buffers of no rows may be null)
+  if (!x || !routed_out) return fail(DSMOE_ERR_INVALID, "forward: null pointer");
   const dsmoe_config& cf = c->cfg;
   if (!w->router_f16 || !w->gate || !w->up || !w->down) return fail(DSMOE_ERR_INVALID, "forward: missing routed weights");
   if (cf.has_bias && !w->bias) return fail(DSMOE_ERR_INVALID, "forward: has_bias without bias");
   if (cf.shared_fmt >= 0 && (!w->sh_gate || !w->sh_up || !w->sh_down || !shared_out))
     return fail(DSMOE_ERR_INVALID, "forward: missing shared expert weights or output");
-  if (T == 0) return DSMOE_OK;
   const int d = cf.d_model, I = cf.d_ff, K = cf.top_k, Is = cf.d_ff_shared, E = cf.n_expert;
   int32_t* sel = selected ? selected : c->selected;
   float* wts = weights ? weights : c->weights;

@@ -111,8 +111,10 @@ size_t dsmoe_scratch_bytes(const dsmoe_ctx* ctx);
  * hc_expand's input is shared_out + routed_out (session.rs:2157-2175).
  * T <= 8 runs three launches (router logits + quantized x | routing, routed
  * and shared gate/up and quantized mid | routed and shared down); larger T
- * sorts the pairs by expert and runs grouped GEMMs.  Calls that overlap on
- * one context race (they share its scratch and row counters). */
+ * sorts the pairs by expert and runs grouped GEMMs.  T = 0 returns
+ * DSMOE_OK without reading or writing anything (the token buffers may then be
+ * NULL).  Calls that overlap on one context race (they share its scratch and
+ * row counters). */
 int dsmoe_forward(dsmoe_ctx* ctx, const dsmoe_weights* w, const float* x, int32_t T,
                   float* shared_out, float* routed_out, int32_t* selected, float* weights,
                   dsmoe_stream_t stream);

@@ -1055,3 +1055,28 @@ def test_hc_ffn_prenorm_chain(gpu):
     assert bits_equal(np_(mix), m)
     ws, wc, wn = O.hc_split_norm(m, scale, base, hc, nw, n, T, 20, 1e-6, 1e-6)
     assert bits_equal(np_(split), ws) and bits_equal(np_(cur), wc) and bits_equal(np_(norm), wn)
+
+
+def test_forward_empty_and_oversized_batches(gpu):
+    """T = 0 is a no-op that returns success and writes nothing; a batch
+    larger than the context's max_tokens is refused before any launch, on
+    the decode and the batch context alike."""
+    import torch
+    case = C.CASES["c1"]
+    w = C.make_weights(case, device=gpu)
+    d, k = case.cfg.d_model, case.cfg.top_k
+    for max_t in (8, 64):
+        say(f"empty / oversized batch, max_tokens={max_t}")
+        lay = dsmoe.MoeLayer(case.cfg, max_t)
+        x = C.make_x(case, T=max_t + 1, device=gpu)
+        so = torch.full((max_t + 1, d), float("nan"), device=gpu)
+        ro = torch.full((max_t + 1, d), float("nan"), device=gpu)
+        sel = torch.full((max_t + 1, k), -7, dtype=torch.int32, device=gpu)
+        lay.forward(w, x[:0], so[:0], ro[:0], sel[:0])
+        torch.cuda.synchronize()
+        assert torch.isnan(so).all() and torch.isnan(ro).all() and (sel == -7).all()
+        with pytest.raises(dsmoe.DsmoeError):
+            lay.forward(w, x, so, ro, sel)
+        torch.cuda.synchronize()
+        assert torch.isnan(ro).all() and (sel == -7).all()
+        lay.close()
