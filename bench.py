@@ -302,7 +302,7 @@ def cpu_baseline(case, hw, xs, seconds, cores, tokens=None):
 # Tokens per CPU oracle call (every core, 1 thread): c1, c3 and c4 in full at
 # every core; c5 (2048 tokens, ~1 min per call at 16 threads) on its first
 # 64; 1-thread runs on the first 4 tokens of the batch configs.
-CPU_TOKENS = {"c1": (None, None), "c2": (None, None), "c3": (None, 4), "c4": (None, 4), "c5": (64, 4),
+CPU_TOKENS = {"c1": (None, None), "c2": (None, None), "c3": (None, 4), "c4": (None, 4), "c4tie": (None, 4), "c5": (64, 4),
               "c5logit": (64, 4)}
 
 
@@ -340,7 +340,11 @@ def case_host_weights(case, hw_full, dev):
     if hw_full is not None and case.cfg == C.C2_CFG and case.seed == C.CASES["c2"].seed:
         E, d = case.cfg.n_expert, case.cfg.d_model
         seed = case.seed
-        router = dsmoe.synth(dsmoe.FMT_F16, seed, C.TID_ROUTER, 1, E, d, sigma=0.02, device="cpu")
+        if case.router_tie:  # every expert's router row the same: routing decided by the bias and ties
+            row = dsmoe.synth(dsmoe.FMT_F16, seed, C.TID_ROUTER, 1, 1, d, sigma=0.02, device="cpu")
+            router = row.reshape(1, d).expand(E, d).contiguous()
+        else:
+            router = dsmoe.synth(dsmoe.FMT_F16, seed, C.TID_ROUTER, 1, E, d, sigma=0.02, device="cpu")
         bias = dsmoe.synth(dsmoe.FMT_F32, seed, C.TID_BIAS, 1, 1, E, sigma=0.01, device="cpu").reshape(E).clone()
         if case.zipf > 0 and case.zipf_logit:
             prior = torch.from_numpy(C.zipf_bias(E, case.zipf, seed)).to(torch.float16)
@@ -373,7 +377,7 @@ def main():
                     help="configs of the prefill measurement added to the line, comma-separated ('none' to skip); "
                          "c5 is reported under prefill, the others under prefill_variants")
     ap.add_argument("--prefill-steps", type=int, default=10)
-    ap.add_argument("--other-configs", default="c1,c3,c4",
+    ap.add_argument("--other-configs", default="c1,c3,c4,c4tie",
                     help="configs also timed on the same path, reported under other_configs ('none' to skip)")
     ap.add_argument("--no-peaks", action="store_true", help="skip the on-box MFMA / HBM peak probes")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timing of the decode step")
@@ -502,7 +506,9 @@ def main():
         for name in [n for n in args.other_configs.split(",") if n and n != args.config]:
             oc = C.CASES[name]
             print(f"[bench] config {name}", file=sys.stderr, flush=True)
-            same = oc.cfg == cfg and oc.seed == case.seed and oc.d_ff_real == case.d_ff_real
+            # the decode config's weights serve configs of the same layer and router
+            same = (oc.cfg == cfg and oc.seed == case.seed and oc.d_ff_real == case.d_ff_real and
+                    oc.router_tie == case.router_tie and oc.zipf == case.zipf and oc.zipf_logit == case.zipf_logit)
             if same:
                 ow = layers if oc.T <= 8 else layers[:1]
             else:  # decode-sized configs rotate over enough copies to exceed the 256 MB last-level cache

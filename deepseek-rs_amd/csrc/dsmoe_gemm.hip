@@ -208,6 +208,7 @@ void dsmoe_gu_grouped(const GuGroupedArgs a) {
   __shared__ u32x4 s_lsign[16 * 128];
   __shared__ uint32_t s_pair[kGuBM], s_xrow[kGuBM], s_qrow[kGuBM];
 
+  if (a.path && (*a.path & a.path_mask) != a.path_want) return;
   const TileSlab ts = xcd_tile_slab((int)a.tile_offsets[a.E], a.I / kGuBN);
   if (!ts.ok) return;
   const int t = ts.t;
@@ -454,6 +455,7 @@ void dsmoe_dn_grouped(const DnGroupedArgs a) {
   __shared__ __align__(16) float s_yd0[kGuBM], s_yd1[kGuBM];
   __shared__ uint32_t s_pair[kGuBM], s_mrow[kGuBM], s_qrow[kGuBM], s_brow[kGuBM];
 
+  if (a.path && (*a.path & a.path_mask) != a.path_want) return;
   const TileSlab ts = xcd_tile_slab((int)a.tile_offsets[a.E], a.d / kDnBN);
   if (!ts.ok) return;
   const int t = ts.t;

@@ -606,6 +606,32 @@ int dsmoe_dispatch(const int32_t* selected, int32_t pairs, int32_t E, int32_t bl
   return launch(K_DISPATCH, dim3(1), dim3(1024), 0, stream, a);
 }
 
+}  // extern "C"
+
+// The forward pass enqueues both the expert-major and the grouped launches of
+// a batch with few pairs per expert and lets the device pick (dsmoe_choose_path);
+// while a PathScope is open, the four batch launchers below tag their
+// arguments with the flag word and the value their workgroups need.
+namespace {
+struct PathSel {
+  const uint32_t* path = nullptr;
+  uint32_t mask = 0, want = 0;
+};
+thread_local PathSel t_path;
+struct PathScope {
+  PathScope(const uint32_t* p, uint32_t m, uint32_t w) { t_path = PathSel{p, m, w}; }
+  ~PathScope() { t_path = PathSel{}; }
+};
+template <typename A>
+void tag_path(A& a) {
+  a.path = t_path.path;
+  a.path_mask = t_path.mask;
+  a.path_want = t_path.want;
+}
+}  // namespace
+
+extern "C" {
+
 // 1-D grid of the grouped kernels: ny slabs for each of 8 * ceil(tiles / 8)
 // tile slots (the kernels' xcd_items mapping; it also covers the tiles x ny
 // items of a grid with fewer than 8 tiles).
@@ -626,6 +652,7 @@ int dsmoe_gate_up_mid_sorted(const void* gate, const void* up, const uint16_t* x
   if (pairs == 0) return DSMOE_OK;
   GuGroupedArgs a{(const uint8_t*)gate, (const uint8_t*)up, xh, (const uint8_t*)xq, sorted_pairs, offsets,
                   tile_offsets, tile_experts, tile_starts, weights, mid_out, d, I, k, E, clamp};
+  tag_path(a);
   // tiles per expert <= ceil(count / BM): at most pairs / BM + one partial tile per used expert
   const int max_tiles = pairs / kGuBM + std::min(E, pairs);
   return launch(K_GU_GROUPED, dim3(xcd_grid(max_tiles, I / kGuBN)), dim3(kGuThreads), 0, stream, a);
@@ -645,6 +672,7 @@ int dsmoe_down_sorted(const void* down, const int8_t* m8, const uint16_t* bsum_h
   if (pairs == 0) return DSMOE_OK;
   DnGroupedArgs a{(const uint8_t*)down, m8, bsum_h, (const uint8_t*)mq, sorted_pairs, offsets, tile_offsets,
                   tile_experts, tile_starts, down_out, d, I, E};
+  tag_path(a);
   const int max_tiles = pairs / kGuBM + std::min(E, pairs);
   return launch(K_DN_GROUPED, dim3(xcd_grid(max_tiles, d / kDnBN)), dim3(kDnThreads), 0, stream, a);
 }
@@ -671,6 +699,7 @@ int dsmoe_gate_up_mid_em(const void* gate, const void* up, const void* xq, const
   m.tile_starts = tile_starts;
   m.tiles = (I + 31) / 32;
   m.np = block_m;
+  tag_path(m);
   const int64_t units = (int64_t)(pairs / block_m + std::min(E, pairs)) * m.tiles;
   if (units > 0x7FFFFFFF) return fail(DSMOE_ERR_UNSUPPORTED, "gate_up_mid_em: too many pairs");
   return launch(K_UP_EM, dim3((unsigned)units), dim3(256), gate_up_em_lds(d / 256, block_m), stream, m);
@@ -697,6 +726,7 @@ int dsmoe_down_em(const void* down, const void* mq, const uint32_t* sorted_pairs
   m.tile_starts = tile_starts;
   m.tiles = (d + kDnEmRows - 1) / kDnEmRows;
   m.np = block_m;
+  tag_path(m);
   const int64_t units = (int64_t)(pairs / block_m + std::min(E, pairs)) * m.tiles;
   if (units > 0x7FFFFFFF) return fail(DSMOE_ERR_UNSUPPORTED, "down_em: too many pairs");
   return launch(K_DN_EM, dim3((unsigned)units), dim3(256), down_em_lds(I / 256, block_m), stream, m);
@@ -860,6 +890,7 @@ struct dsmoe_ctx {
   uint32_t* g_tile_offsets64 = nullptr;
   uint32_t* g_tile_experts64 = nullptr;
   uint32_t* g_tile_starts64 = nullptr;
+  uint32_t* g_path = nullptr;  // dsmoe_choose_path's flags (expert-major or grouped, per launch)
   float* q80_part = nullptr;     // split shared-expert GEMM partials, [kQ80MaxSplit][min(T, 256)][cols]
   uint16_t* shw_h[3] = {};       // shared gate / up / down unpacked for dsmoe_q80_wide (codes as f16)
   // Batches on the wide shared-expert path run the quantization of x and the
@@ -1050,6 +1081,7 @@ int dsmoe_create(const dsmoe_config* cfg, int32_t max_tokens, dsmoe_ctx** out) {
     A(&c->g_tile_offsets64, (E + 1) * 4);
     A(&c->g_tile_experts64, max_tiles64 * 4);
     A(&c->g_tile_starts64, max_tiles64 * 4);
+    A(&c->g_path, 16);
     A(&c->q80_part, (size_t)kQ80MaxSplit * std::min<size_t>(T, 256) * std::max<size_t>(2 * Is, d) * 4);
     if (cfg->shared_fmt == 0 && q80_wide_fits((int)d, cfg->d_ff_shared) && max_tokens >= q80_wide_min_t()) {
       const size_t is = (size_t)cfg->d_ff_shared;
@@ -1116,13 +1148,16 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // runs the matvec launches, one work item per (row tile, pair / token).
   const bool grouped = T > kDecodeMaxT && c->xh != nullptr;
   // Few pairs per expert (at most kEmMaxLoad on average): the routed experts
-  // stream their weights once per chunk of em_pairs() pairs
+  // may stream their weights once per chunk of em_pairs() pairs
   // (expert-major matvec) instead of dequantizing them into MFMA tiles.
+  // Both forms are enqueued and the device picks one from the sorted pairs
+  // (dsmoe_choose_path): a skewed batch (a few experts holding most pairs)
+  // runs grouped even at a low average load.
   const bool em = grouped && (int64_t)P <= (int64_t)kEmMaxLoad * E && em_fits(cf);
   // The int8 grouped down overtakes the expert-major one from about 2 pairs
-  // per expert (c4, 4 per expert: 386 against 526 us), well before the
-  // gate/up does.
-  const bool em_dn = em && (int64_t)P <= (int64_t)kEmDnMaxLoad * E;
+  // per expert on average (c4, 4 per expert: 386 against 526 us), well before
+  // the gate/up does.
+  const bool dn_floor = (int64_t)P > (int64_t)kEmDnMaxLoad * E;
   // Large batches run the shared expert through the unpacked wide GEMM, over
   // the caller's unpacked matrices when the weights carry them (all six
   // pointers), else over the context's copies unpacked in this call.
@@ -1152,7 +1187,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   {
     StageScope sc(c, DSMOE_STAGE_PREP, stream);
     RouterLogitsArgs r{(const uint16_t*)w->router_f16, x, c->logits, d, E, T};
-    Q8KArgs q8k{x, c->xq8k, d, T, grouped && !em ? c->xh : nullptr};
+    Q8KArgs q8k{x, c->xq8k, d, T, grouped ? c->xh : nullptr};
     Q80Args q80{x, c->xq80, c->xs80, d, T, grouped ? c->xh80 : nullptr};
     if (fork) {  // the router here, the quantizations on the side stream
       DSM_TRY(prep_impl(&r, nullptr, nullptr, stream));
@@ -1171,12 +1206,20 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
                                        wts, stream));
     else
       DSM_TRY(dsmoe_router_select(&cf, c->logits, w->bias, T, nullptr, sel, wts, stream));
-    if (grouped)  // moe_count/prefix/scatter_sorted_pairs + tiles (moe.rs:299-362, 547-596)
-      DSM_TRY(dsmoe_dispatch(sel, P, E, em ? em_pairs() : kGuBM, c->g_counts, c->g_offsets, c->g_sorted,
+    if (grouped && !em)  // moe_count/prefix/scatter_sorted_pairs + tiles (moe.rs:299-362, 547-596)
+      DSM_TRY(dsmoe_dispatch(sel, P, E, kGuBM, c->g_counts, c->g_offsets, c->g_sorted,
                              c->g_tile_offsets, c->g_tile_experts, c->g_tile_starts, stream));
-    if (em && !em_dn)  // the same sort again, cut into the grouped down's tiles
-      DSM_TRY(dsmoe_dispatch(sel, P, E, kGuBM, c->g_counts, c->g_offsets, c->g_sorted, c->g_tile_offsets64,
-                             c->g_tile_experts64, c->g_tile_starts64, stream));
+    if (em) {  // the sort cut into em_pairs() and into 64-pair tiles, and the choice between the two
+      DispatchArgs da{sel, c->g_counts, c->g_offsets, c->g_sorted, c->g_tile_offsets, c->g_tile_experts,
+                      c->g_tile_starts, P, E, em_pairs()};
+      da.tile_offsets2 = c->g_tile_offsets64;
+      da.tile_experts2 = c->g_tile_experts64;
+      da.tile_starts2 = c->g_tile_starts64;
+      da.block_m2 = kGuBM;
+      da.path_flags = c->g_path;
+      da.dn_grouped = dn_floor ? 1 : 0;
+      DSM_TRY(launch(K_DISPATCH, dim3(1), dim3(1024), 0, stream, da));
+    }
   }
   // 3. routed + shared gate/up/SwiGLU              (session.rs:1910-1959, 2075-2112)
   // The row-streaming launch also quantizes the mid rows (step 4) when the
@@ -1204,9 +1247,16 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
       return fail(DSMOE_ERR_HIP, "forward: wait for the quantization of x");
     if (em) {
       StageScope sg(c, DSMOE_STAGE_GU_GROUPED, stream);
-      DSM_TRY(dsmoe_gate_up_mid_em(w->gate, w->up, c->xq8k, c->g_sorted, c->g_offsets, c->g_tile_offsets,
-                                   c->g_tile_experts, c->g_tile_starts, wts, c->mid, d, I, K, E, P,
-                                   em_pairs(), cf.swiglu_clamp, stream));
+      {
+        PathScope ps(c->g_path, 1u, 0u);
+        DSM_TRY(dsmoe_gate_up_mid_em(w->gate, w->up, c->xq8k, c->g_sorted, c->g_offsets, c->g_tile_offsets,
+                                     c->g_tile_experts, c->g_tile_starts, wts, c->mid, d, I, K, E, P,
+                                     em_pairs(), cf.swiglu_clamp, stream));
+      }
+      PathScope ps(c->g_path, 1u, 1u);
+      DSM_TRY(dsmoe_gate_up_mid_sorted(w->gate, w->up, c->xh, c->xq8k, c->g_sorted, c->g_offsets,
+                                       c->g_tile_offsets64, c->g_tile_experts64, c->g_tile_starts64, wts, c->mid, d,
+                                       I, K, E, P, cf.swiglu_clamp, stream));
     } else if (grouped) {
       StageScope sg(c, DSMOE_STAGE_GU_GROUPED, stream);
       DSM_TRY(dsmoe_gate_up_mid_sorted(w->gate, w->up, c->xh, c->xq8k, c->g_sorted, c->g_offsets, c->g_tile_offsets,
@@ -1257,7 +1307,7 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
   // 4. Q8_K(mid) + Q8_0 / Q8_K of the shared mid  (session.rs:1964-1976, 2114-2127)
   if (!fuse_midq) {
     StageScope sc(c, DSMOE_STAGE_MIDQ, stream);
-    Q8KArgs qa{c->mid, c->midq, I, P, nullptr, grouped && !em_dn ? c->m8 : nullptr, grouped && !em_dn ? c->bsh : nullptr};
+    Q8KArgs qa{c->mid, c->midq, I, P, nullptr, grouped ? c->m8 : nullptr, grouped ? c->bsh : nullptr};
     Q8KArgs qb{c->sh_mid, c->sh_midq, Is, T};
     Q80Args q80{c->sh_mid, c->sh_q80, c->sh_s80, Is, T, grouped ? c->shh : nullptr};
     if (fork) {  // the shared mid is quantized on the side stream
@@ -1280,14 +1330,18 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     if (grouped) {
       {
         StageScope sg(c, DSMOE_STAGE_DN_GROUPED, stream);
-        if (em_dn) {
-          DSM_TRY(dsmoe_down_em(w->down, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets, c->g_tile_experts,
-                                c->g_tile_starts, c->down_out, d, I, E, P, em_pairs(), stream));
+        if (em) {
+          {
+            PathScope ps(c->g_path, 2u, 0u);
+            DSM_TRY(dsmoe_down_em(w->down, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets,
+                                  c->g_tile_experts, c->g_tile_starts, c->down_out, d, I, E, P, em_pairs(), stream));
+          }
+          PathScope ps(c->g_path, 2u, 2u);
+          DSM_TRY(dsmoe_down_sorted(w->down, c->m8, c->bsh, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets64,
+                                    c->g_tile_experts64, c->g_tile_starts64, c->down_out, d, I, E, P, stream));
         } else {
-          DSM_TRY(dsmoe_down_sorted(w->down, c->m8, c->bsh, c->midq, c->g_sorted, c->g_offsets,
-                                    em ? c->g_tile_offsets64 : c->g_tile_offsets,
-                                    em ? c->g_tile_experts64 : c->g_tile_experts,
-                                    em ? c->g_tile_starts64 : c->g_tile_starts, c->down_out, d, I, E, P, stream));
+          DSM_TRY(dsmoe_down_sorted(w->down, c->m8, c->bsh, c->midq, c->g_sorted, c->g_offsets, c->g_tile_offsets,
+                                    c->g_tile_experts, c->g_tile_starts, c->down_out, d, I, E, P, stream));
         }
       }
       DSM_TRY(dsmoe_moe_sum(c->down_out, routed_out, d, K, T, stream));

@@ -173,6 +173,10 @@ struct GuEmArgs {
   const uint32_t* tile_starts;
   int32_t tiles;                 // row tiles of 32 rows
   int32_t np;                    // the dispatch's block_m (pairs per chunk), 1..kEmPairs
+  // set by the forward pass when the expert-major and the grouped launches are
+  // both enqueued: the workgroups return unless (*path & path_mask) == path_want
+  const uint32_t* path = nullptr;
+  uint32_t path_mask = 0, path_want = 0;
 };
 struct DnEmArgs {
   DownArgs dn;    // selected and out unused; down_out [pairs][d]
@@ -183,7 +187,19 @@ struct DnEmArgs {
   const uint32_t* tile_starts;
   int32_t tiles;                 // row tiles of kDnEmRows rows
   int32_t np;                    // the dispatch's block_m (pairs per chunk), 1..kEmPairs
+  // set by the forward pass when the expert-major and the grouped launches are
+  // both enqueued: the workgroups return unless (*path & path_mask) == path_want
+  const uint32_t* path = nullptr;
+  uint32_t path_mask = 0, path_want = 0;
 };
+
+// The launches of a batch with few pairs per expert on average are chosen on
+// the device once the pairs are sorted (dsmoe_dispatch with a second tiling
+// and path_flags): the expert-major kernels stream an expert's weights once
+// per chunk of up to em_pairs pairs, the grouped ones once per 64-pair tile,
+// so skewed loads (a few experts holding most pairs) go grouped.
+// path_flags[0]: bit 0 gate/up grouped, bit 1 down grouped (also when
+// dn_grouped: the average load alone favours it).
 
 // Largest token count of the row-streaming (decode) launches.
 constexpr int32_t kMaxDecodeT = 8;
@@ -205,6 +221,10 @@ struct GuGroupedArgs {
   float* mid;                     // [P][I]
   int32_t d, I, k, E;
   float clamp;
+  // set by the forward pass when the expert-major and the grouped launches are
+  // both enqueued: the workgroups return unless (*path & path_mask) == path_want
+  const uint32_t* path = nullptr;
+  uint32_t path_mask = 0, path_want = 0;
 };
 enum : int32_t { kGuBM = 64, kGuThreads = 512, kGuBN = kGuThreads / 2 };
 
@@ -223,6 +243,10 @@ struct DnGroupedArgs {
   const uint32_t* tile_starts;
   float* down_out;                // [P][d]
   int32_t d, I, E;
+  // set by the forward pass when the expert-major and the grouped launches are
+  // both enqueued: the workgroups return unless (*path & path_mask) == path_want
+  const uint32_t* path = nullptr;
+  uint32_t path_mask = 0, path_want = 0;
 };
 enum : int32_t { kDnThreads = 256, kDnBN = kDnThreads / 2 };  // 4 waves: three workgroups per CU at 168 VGPRs
 
@@ -355,6 +379,14 @@ struct DispatchArgs {
   uint32_t* tile_experts;   // [max tiles] or null
   uint32_t* tile_starts;    // [max tiles] or null
   int32_t pairs, E, block_m;
+  // optional second tiling of the same sort (block_m2 pairs per tile) and
+  // the expert-major / grouped choice from the two tile counts (ChooseArgs)
+  uint32_t* tile_offsets2 = nullptr;
+  uint32_t* tile_experts2 = nullptr;
+  uint32_t* tile_starts2 = nullptr;
+  int32_t block_m2 = 0;
+  uint32_t* path_flags = nullptr;
+  int32_t dn_grouped = 0;
 };
 
 // Synthetic weights: N(0, sigma) from a counter-based generator, quantized

@@ -1929,6 +1929,7 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_dn_rows(const DnArgs a) 
 // return at once.
 extern "C" __global__ __launch_bounds__(256) void dsmoe_up_em(const GuEmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
+  if (a.path && (*a.path & a.path_mask) != a.path_want) return;
   const int tile = blockIdx.x % a.tiles, chunk = blockIdx.x / a.tiles;
   if (chunk >= (int)a.tile_offsets[a.gu.E]) return;
   const int e = (int)a.tile_experts[chunk];
@@ -1948,8 +1949,10 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_up_em(const GuEmArgs a) 
 
 extern "C" __global__ __launch_bounds__(256) void dsmoe_dn_em(const DnEmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
+  if (a.path && (*a.path & a.path_mask) != a.path_want) return;
   role_down_em(a, blockIdx.x % a.tiles, blockIdx.x / a.tiles, smem);
 }
+
 
 // Hash routing (moe.rs:92-109, weights :143-159), one workgroup per token:
 // the probabilities of all experts, then thread 0 reads the token's row of
@@ -2295,17 +2298,31 @@ extern "C" __global__ __launch_bounds__(1024) void dsmoe_dispatch(const Dispatch
       __builtin_amdgcn_wave_barrier();
     }
   }
-  if (a.tile_offsets) {
+  auto tiles = [&](uint32_t bm, uint32_t* tile_offsets, uint32_t* tile_experts, uint32_t* tile_starts) {
     __syncthreads();
-    const uint32_t bm = (uint32_t)a.block_m;
     if (wv == 0) wave_exclusive_scan(s_tot, s_scan, E, [bm](uint32_t c) { return (c + bm - 1) / bm; });
     __syncthreads();
-    for (int e = threadIdx.x; e <= E; e += blockDim.x) a.tile_offsets[e] = s_scan[e];
+    for (int e = threadIdx.x; e <= E; e += blockDim.x) tile_offsets[e] = s_scan[e];
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
       const uint32_t n = (s_tot[e] + bm - 1) / bm;
       for (uint32_t t = 0; t < n; t++) {
-        a.tile_experts[s_scan[e] + t] = (uint32_t)e;
-        a.tile_starts[s_scan[e] + t] = t * (uint32_t)a.block_m;
+        tile_experts[s_scan[e] + t] = (uint32_t)e;
+        tile_starts[s_scan[e] + t] = t * bm;
+      }
+    }
+    return s_scan[E];  // the tile count (every thread reads it before the next scan)
+  };
+  if (a.tile_offsets) {
+    const uint32_t n1 = tiles((uint32_t)a.block_m, a.tile_offsets, a.tile_experts, a.tile_starts);
+    if (a.tile_offsets2) {
+      const uint32_t n2 = tiles((uint32_t)a.block_m2, a.tile_offsets2, a.tile_experts2, a.tile_starts2);
+      // Expert-major (tiling 1) or grouped (tiling 2).  Measured on MI355X
+      // (k = 8, E = 256, uniform and skewed loads): an expert-major chunk of
+      // up to 4 pairs costs about 4/7 of a grouped 64-pair tile (c4: 376
+      // chunks against 251 tiles, 0.84 against 0.97 ms of gate/up).
+      if (a.path_flags && threadIdx.x == 0) {
+        const uint32_t gu = 4u * n1 > 7u * n2 ? 1u : 0u;
+        a.path_flags[0] = gu | ((gu || a.dn_grouped) ? 2u : 0u);
       }
     }
   }
