@@ -1276,6 +1276,9 @@ static int forward_impl(dsmoe_ctx* c, const dsmoe_weights* w, const float* x, in
     if (cf.shared_fmt >= 0) { a.sh_tiles = s2.tiles; a.sh_work = T; }
     if (up_rows && cf.shared_fmt == 0) {  // Q8_0 row-streaming tiles: 4 rows of gate and of up
       a.sh_tiles = q80_rows_tiles(Is, true);
+      // the start delay of the shared expert's workgroups: for a shared
+      // gate/up of 16 MB and more (c2: 31 MB), none below (c1: 6 MB)
+      a.sh_delay = (int64_t)2 * Is * (d / 32) * 34 >= ((int64_t)16 << 20) ? 1 : 0;
       lds = std::max(lds, q80_rows_lds(d / 32));
     }
     if (grouped && cf.shared_fmt == 0) {  // shared expert as a GEMM over the whole batch

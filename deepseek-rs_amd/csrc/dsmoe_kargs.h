@@ -139,6 +139,7 @@ struct UpArgs {
   Q80Args sh_midq{};
   uint32_t* mid_cnt = nullptr;
   int32_t fuse_midq = 0;
+  int32_t sh_delay = 0;  // nonzero: the Q8_0 shared expert's workgroups start about 8 us late
 };
 
 // Q8_K of the routed mid rows (+ the IQ2 shared mid) and Q8_0 of the shared mid.

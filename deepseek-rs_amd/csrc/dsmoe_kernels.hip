@@ -1848,14 +1848,18 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_up_rows(const UpArgs a) 
   if (w < a.sh_tiles * a.sh_work) {
     const int tile = w % a.sh_tiles, tok = w / a.sh_tiles;
     if (a.sh_fmt == 0) {
-      // The shared expert's workgroups start about 8 us (2 x 127 x 64
-      // cycles) late: the routed workgroups first load the logits and the
-      // activation words, which otherwise queue behind this 31 MB stream
-      // (the routing sits on the routed path, the shared rows do not).
-      // Measured per decode step at c2: 53.4-53.9 us without, 52.1-52.8 with
-      // this delay; 2, 4, 12 and 16 us were worse or equal.
-      __builtin_amdgcn_s_sleep(127);
-      __builtin_amdgcn_s_sleep(127);
+      // With a large shared expert its workgroups start about 8 us (2 x 127
+      // x 64 cycles) late: the routed workgroups first load the logits and
+      // the activation words, which otherwise queue behind its stream (the
+      // routing sits on the routed path, the shared rows do not).  Measured
+      // per decode step at c2 (31 MB of shared gate/up): 53.4-53.9 us
+      // without, 52.1-52.8 with this delay; 2, 4, 12 and 16 us were worse
+      // or equal.  At c1 (6 MB) the delay only lengthens the launch
+      // (29.0 against 30.6 us per step), so the host sets it by size.
+      if (a.sh_delay) {
+        __builtin_amdgcn_s_sleep(127);
+        __builtin_amdgcn_s_sleep(127);
+      }
       role_q80_rows_any(a.sh_q80, tile, tok, smem);
       if (a.fuse_midq) {
         const int Is = a.sh_q80.out_dim, RT = 4, ng = (Is + 255) >> 8, row0 = tile * RT, g = row0 >> 8;
