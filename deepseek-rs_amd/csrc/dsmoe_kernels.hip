@@ -860,17 +860,18 @@ __device__ __forceinline__ size_t gate_up_rows_lds(int nb) {
 __device__ __forceinline__ float iq2_blk_dot(const uint32_t* w, uint32_t sel, uint32_t dsh, const uint8_t* q8, float yd,
                                              const Iq2Tables* t) {
   int32_t bsum = 0;
+  int zo = 0;
 #pragma unroll
   for (int ib = 0; ib < 8; ib++) {
-    // opaque zero depending on the running sum (as in iq2_block_dot): the
-    // sub-block's lookups stay after the previous one's arithmetic, which
-    // holds the kernel to ~116 VGPRs (4 waves per SIMD) instead of 254
-    int z = 0;
-    asm volatile("" : "+v"(z) : "v"(bsum));
-    const uint32_t aux0 = __builtin_amdgcn_perm(w[2 * ib + 1], w[2 * ib], sel) + z;
-    const uint32_t aux1 = __builtin_amdgcn_perm(w[2 * ib + 2], w[2 * ib + 1], sel) + z;
-    const uint4 qa = *(const uint4*)(q8 + ib * 32 + z);
-    const uint4 qb = *(const uint4*)(q8 + ib * 32 + 16 + z);
+    // sel and zo (always 0) pass through an empty asm that depends on the
+    // running sum: the sub-block's lookups stay after the previous one's
+    // arithmetic, which holds the kernel to ~116 VGPRs (4 waves per SIMD)
+    // instead of 254, at no instruction for sel and one add for zo
+    asm volatile("" : "+v"(sel), "+v"(zo) : "v"(bsum));
+    const uint32_t aux0 = __builtin_amdgcn_perm(w[2 * ib + 1], w[2 * ib], sel);
+    const uint32_t aux1 = __builtin_amdgcn_perm(w[2 * ib + 2], w[2 * ib + 1], sel);
+    const uint4 qa = *(const uint4*)(q8 + ib * 32 + zo);
+    const uint4 qb = *(const uint4*)(q8 + ib * 32 + 16 + zo);
     int32_t pos = 0, neg = 0;
     const uint32_t qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
@@ -883,8 +884,14 @@ __device__ __forceinline__ float iq2_blk_dot(const uint32_t* w, uint32_t sel, ui
       neg = dot4((uint32_t)((gv & mv) >> 32), qv[2 * g + 1], neg);
     }
     const int32_t ls = (int32_t)((aux1 >> 27) | 1u);
+    // bsum += sumi * ls as one v_mad_i32_i24: |sumi| <= 3 * 32 * 43 * 128 <
+    // 2^23 and ls <= 31 are inside its signed 24-bit operand range, so the
+    // product is the exact one (__mul24 costs four more instructions of sign
+    // extension).  The asm reads only sumi and ls, never a dot4 result: the
+    // compiler inserts the wait states a DOT result needs before a VALU read
+    // for its own instructions only, not for operands of inline asm.
     const int32_t sumi = pos - neg - neg;
-    bsum += __mul24(sumi, ls);  // |sumi| < 2^18, ls <= 31: one v_mad_i32_i24
+    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(bsum) : "v"(sumi), "v"(ls), "v"(bsum));
   }
   const float xd = f16_to_f32_ftz((uint16_t)(w[0] >> dsh));
   return 0.125f * xd * yd * (float)bsum;
