@@ -1117,8 +1117,9 @@ __device__ __forceinline__ float f16_to_f32_ftz_hw(uint16_t h) {
 // most compute units idle and the launch lasts one workgroup's time.
 template <int NE, int NT>
 __device__ __forceinline__ void router_tile(const RouterLogitsArgs& a) {
-  constexpr int NR = NE * 8;  // tree rows per half
-  __shared__ float part[NR][256];  // [expert * 8 + token][tx], eight tokens at a time
+  constexpr int R = NE * NT;  // rows (expert-major: e * NT + t)
+  static_assert(R % 4 == 0, "rows split in quarters");
+  __shared__ float xch[4][R / 2][64];  // [wave][row][lane]: partials handed to the partner wave
   const int neg = (a.E + NE - 1) / NE;
   const int e0 = (blockIdx.x % neg) * NE, t0 = (blockIdx.x / neg) * NT;
   const int tx = threadIdx.x, d = a.d, nb = d >> 8;
@@ -1172,24 +1173,58 @@ __device__ __forceinline__ void router_tile(const RouterLogitsArgs& a) {
     load(0, j + 2);
     products(1);
   }
+  // The halving tree p[i] += p[i + s], s = 128, 64, ..., 1, over the 256
+  // partials of each of the R rows (p[i] = thread i's sum; wave w holds
+  // i = 64 w + lane).  Every node is the same f32 sum of the same two
+  // children as in a tree over LDS, so the bits are too; only the schedule
+  // differs.  s = 128 pairs wave w with w ^ 2: each keeps half of the rows
+  // and receives the partner's partials of them through LDS.  s = 64 pairs
+  // w with w ^ 1 on a quarter of the rows the same way.  s = 32 .. 1 stay
+  // inside the wave (lane i < s adds lane i + s: permlane swaps for 32 and
+  // 16, DPP row shifts for 8 .. 1) and lane 0 ends with each row's sum.
+  const int w = __builtin_amdgcn_readfirstlane(tx >> 6), lane = tx & 63;
+  float v1[R / 2];
+  {
+    const bool hi = w >= 2;  // keeps rows R/2 .. R-1
 #pragma unroll
-  for (int h = 0; h < NT / 8; h++) {
-    if (h) __syncthreads();  // the previous half's tree is read out
-#pragma unroll
-    for (int e = 0; e < NE; e++)
-#pragma unroll
-      for (int t = 0; t < 8; t++) part[8 * e + t][tx] = acc[e][8 * h + t];
-    __syncthreads();
-    for (int s2 = 128, lg = 7; s2 > 0; s2 >>= 1, lg--) {
-      for (int idx = tx; idx < NR * s2; idx += 256) {
-        const int pr = idx >> lg, i = idx & (s2 - 1);
-        part[pr][i] += part[pr][i + s2];
-      }
-      __syncthreads();
+    for (int r = 0; r < R / 2; r++) {
+      xch[w][r][lane] = hi ? acc[r / NT][r % NT] : acc[(R / 2 + r) / NT][(R / 2 + r) % NT];
+      v1[r] = hi ? acc[(R / 2 + r) / NT][(R / 2 + r) % NT] : acc[r / NT][r % NT];
     }
-    if (tx < NR) {
-      const int e = tx >> 3, t = 8 * h + (tx & 7);
-      if (e0 + e < a.E && t0 + t < a.T) a.out[(size_t)(t0 + t) * a.E + e0 + e] = part[tx][0];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R / 2; r++) v1[r] = v1[r] + xch[w ^ 2][r][lane];
+  __syncthreads();
+  float v2[R / 4];
+  {
+    const bool odd = w & 1;  // keeps the second quarter of its half
+#pragma unroll
+    for (int r = 0; r < R / 4; r++) {
+      xch[w][r][lane] = odd ? v1[r] : v1[R / 4 + r];
+      v2[r] = odd ? v1[R / 4 + r] : v1[r];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R / 4; r++) {
+    float v = v2[r] + xch[w ^ 1][r][lane];
+    const uint32_t vb = __builtin_bit_cast(uint32_t, v);
+    v = v + __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_permlane32_swap(vb, vb, false, false)[1]);
+    const uint32_t vc = __builtin_bit_cast(uint32_t, v);
+    v = v + __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_permlane16_swap(vc, vc, false, false)[1]);
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x108, 0xF, 0xF, false));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x104, 0xF, 0xF, false));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x102, 0xF, 0xF, false));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x101, 0xF, 0xF, false));
+    v2[r] = v;
+  }
+  if (lane == 0) {
+    const int base = (w >= 2 ? R / 2 : 0) + ((w & 1) ? R / 4 : 0);
+#pragma unroll
+    for (int r = 0; r < R / 4; r++) {
+      const int row = base + r, e = row / NT, tt = row % NT;
+      if (e0 + e < a.E && t0 + tt < a.T) a.out[(size_t)(t0 + tt) * a.E + e0 + e] = v2[r];
     }
   }
 }
