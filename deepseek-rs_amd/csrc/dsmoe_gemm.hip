@@ -1092,13 +1092,13 @@ extern "C" __global__ __launch_bounds__(64 * kQwWaves) void dsmoe_q80_wide_swigl
 
 // ---------------------------------------------------------------------------
 // Router logits for batches (matmul_f16, matmul.rs:57-105): workgroup =
-// 8 experts x 16 tokens.  For each (token, expert) thread tx sums elements
+// 8 experts x 12 tokens.  For each (token, expert) thread tx sums elements
 // tx, tx+256, ... in order (f32 multiply, then add), and the halving tree
 // 128 .. 1 over the 256 partials combines them, as in the per-row role of
 // dsmoe_prep; each weight element loaded (and converted from f16, the
-// larger part of the non-product work) serves 16 tokens and each activation
+// larger part of the non-product work) serves 12 tokens and each activation
 // element 8 experts.
-// grid = ceil(E / 8) * ceil(T / 16), 256 threads.
+// grid = ceil(E / 8) * ceil(T / 12), 256 threads.
 // ---------------------------------------------------------------------------
 namespace {
 // f16 bits -> f32 for a product, as f16_to_f32_ftz: the hardware conversion
@@ -1112,9 +1112,11 @@ __device__ __forceinline__ float f16_to_f32_ftz_hw(uint16_t h) {
 }
 }  // namespace
 
-// NE experts x NT tokens per workgroup (NT a multiple of 8): 8 x 16 for
-// large batches; 4 x 8 for small ones, where the grid of 8 x 16 tiles leaves
-// most compute units idle and the launch lasts one workgroup's time.
+// NE experts x NT tokens per workgroup (NE * NT a multiple of 4): 8 x 12 for
+// large batches (165 registers: three waves per SIMD, where 8 x 16 tiles
+// needed 207 and ran two, 4 % slower at T = 2048); 4 x 8 for small ones,
+// where the grid of large tiles leaves most compute units idle and the
+// launch lasts one workgroup's time.
 template <int NE, int NT>
 __device__ __forceinline__ void router_tile(const RouterLogitsArgs& a) {
   constexpr int R = NE * NT;  // rows (expert-major: e * NT + t)
@@ -1229,7 +1231,7 @@ __device__ __forceinline__ void router_tile(const RouterLogitsArgs& a) {
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void dsmoe_router_tile(const RouterLogitsArgs a) { router_tile<8, 16>(a); }
+extern "C" __global__ __launch_bounds__(256) void dsmoe_router_tile(const RouterLogitsArgs a) { router_tile<8, 12>(a); }
 extern "C" __global__ __launch_bounds__(256) void dsmoe_router_tile_s(const RouterLogitsArgs a) { router_tile<4, 8>(a); }
 
 

@@ -312,11 +312,11 @@ static int prep_impl(const RouterLogitsArgs* r, const Q8KArgs* q8k, const Q80Arg
   // the batch kernel addresses x and the router with 32-bit buffer offsets
   if (r && r->T >= kRouterTileMinT && (int64_t)r->T * r->d * 4 < ((int64_t)1 << 31) &&
       (int64_t)r->E * r->d * 2 < ((int64_t)1 << 31)) {
-    // 8 x 16 tiles unless their grid would leave most compute units idle:
-    // below 128 of them (c3, T = 32: 64) the 4 x 8 tiles measured ~1 % faster
-    // per layer, at 256 (c4, T = 128, where the concurrent shared expert is
-    // the longer chain) ~0.6 % slower
-    const unsigned big = (unsigned)(((r->E + 7) / 8) * ((r->T + 15) / 16));
+    // 8 x 12 tiles unless their grid would leave most compute units idle:
+    // below 128 of them (c3, T = 32: 96) the 4 x 8 tiles measured ~1 % faster
+    // per layer, at c4 (T = 128, where the concurrent shared expert is the
+    // longer chain) ~0.6 % slower
+    const unsigned big = (unsigned)(((r->E + 7) / 8) * ((r->T + 11) / 12));
     if (big < 128u)
       DSM_TRY(launch(K_ROUTER_TILE_S, dim3(((r->E + 3) / 4) * ((r->T + 7) / 8)), dim3(256), 0, stream, *r));
     else
