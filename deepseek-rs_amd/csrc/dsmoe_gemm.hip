@@ -1101,15 +1101,9 @@ extern "C" __global__ __launch_bounds__(64 * kQwWaves) void dsmoe_q80_wide_swigl
 // grid = ceil(E / 8) * ceil(T / 12), 256 threads.
 // ---------------------------------------------------------------------------
 namespace {
-// f16 bits -> f32 for a product, as f16_to_f32_ftz: the hardware conversion
-// (exact for normal values and Inf), subnormals flushed to a signed zero.  A
-// signalling NaN comes out quiet where the bit-level conversion keeps it
-// signalling; the value only enters a multiply, which quiets it either way,
-// so the products have the same bits.  Four instructions instead of ten.
-__device__ __forceinline__ float f16_to_f32_ftz_hw(uint16_t h) {
-  const float f = (float)__builtin_bit_cast(_Float16, h);
-  return __builtin_fabsf(f) < 6.103515625e-05f ? __builtin_copysignf(0.0f, f) : f;
-}
+// s_setreg operand for MODE bits 7:6 (the f16 / f64 denormal mode): hwreg id
+// 1, offset 6, size 2
+constexpr int kHwregModeF16F64Denorm = 1 | (6 << 6) | ((2 - 1) << 11);
 }  // namespace
 
 // NE experts x NT tokens per workgroup (NE * NT a multiple of 4): 8 x 12 for
@@ -1120,6 +1114,14 @@ __device__ __forceinline__ float f16_to_f32_ftz_hw(uint16_t h) {
 template <int NE, int NT>
 __device__ __forceinline__ void router_tile(const RouterLogitsArgs& a) {
   constexpr int R = NE * NT;  // rows (expert-major: e * NT + t)
+  // f16 input denormals flushed (MODE bits 7:6 = 0, this wave only): the
+  // hardware widening then gives a signed zero for every f16 subnormal, as
+  // the reference's conversion does, and the exact value for the rest (a
+  // signalling NaN comes out quiet where the bit-level conversion keeps it
+  // signalling; the value only enters a multiply, which quiets it either
+  // way, so the products have the same bits).  f32 arithmetic keeps its own
+  // denormal mode (bits 5:4).
+  __builtin_amdgcn_s_setreg(kHwregModeF16F64Denorm, 0);
   static_assert(R % 4 == 0, "rows split in quarters");
   __shared__ float xch[4][R / 2][64];  // [wave][row][lane]: partials handed to the partner wave
   const int neg = (a.E + NE - 1) / NE;
@@ -1158,7 +1160,7 @@ __device__ __forceinline__ void router_tile(const RouterLogitsArgs& a) {
   auto products = [&](int buf) {
     float wv[NE];
 #pragma unroll
-    for (int k = 0; k < NE; k++) wv[k] = f16_to_f32_ftz_hw(wh[buf][k]);
+    for (int k = 0; k < NE; k++) wv[k] = (float)__builtin_bit_cast(_Float16, wh[buf][k]);  // flushed: MODE
 #pragma unroll
     for (int e = 0; e < NE; e++)
 #pragma unroll

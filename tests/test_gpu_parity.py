@@ -80,7 +80,7 @@ def test_router_logits_bitexact(gpu, E, d, T):
     assert bits_equal(np_(out), want)
 
 
-@pytest.mark.parametrize("T", [3, 40])
+@pytest.mark.parametrize("T", [3, 40, 1030])
 def test_router_logits_special_weights_bitexact(gpu, T):
     """Router weights over the whole finite f16 range with many subnormals
     (flushed to signed zeros by the reference's conversion) and signed zeros,
@@ -96,6 +96,26 @@ def test_router_logits_special_weights_bitexact(gpu, T):
     h |= (rng.random((E, d)) < 0.5).astype(np.uint16) << 15
     w = torch.from_numpy(h.view(np.int16).copy()).to(gpu)
     x = dsmoe.synth(dsmoe.FMT_F32, 1, 2, 1, T, d, sigma=1.0, device=gpu)
+    out = torch.empty(T, E, device=gpu)
+    dsmoe.router_logits(w, x, out, d, E, T)
+    want = O.router_logits(h.reshape(-1).copy(), np_(x), d, E, T, NT)
+    assert bits_equal(np_(out), want)
+
+
+@pytest.mark.parametrize("T", [24, 256])
+def test_router_logits_every_finite_f16_weight(gpu, T):
+    """Every finite f16 bit pattern once as a router weight (E = d = 256: the
+    65,536 patterns, Inf and NaN replaced by zeros), so every subnormal, both
+    zeros and every normal value pass through the tiled kernels' widening;
+    T = 24 runs the small tiles, T = 256 the large ones."""
+    import torch
+    E = d = 256
+    say(f"router_logits every f16 weight T={T}")
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    h[(h & 0x7C00) == 0x7C00] = 0
+    h = h.reshape(E, d)
+    w = torch.from_numpy(h.view(np.int16).copy()).to(gpu)
+    x = dsmoe.synth(dsmoe.FMT_F32, 1, 3, 1, T, d, sigma=1.0, device=gpu)
     out = torch.empty(T, E, device=gpu)
     dsmoe.router_logits(w, x, out, d, E, T)
     want = O.router_logits(h.reshape(-1).copy(), np_(x), d, E, T, NT)
