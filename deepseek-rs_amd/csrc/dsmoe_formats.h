@@ -123,6 +123,13 @@ DSM_HD float f16_to_f32_ftz(uint16_t h) {
   else bits = sign | ((ex + 112u) << 23) | (man << 13);
   return __builtin_bit_cast(float, bits);
 }
+// s_setreg operand for MODE bits 7:6, the f16 / f64 denormal mode (hwreg
+// id 1, offset 6, size 2).  With both bits clear the wave flushes f16 input
+// denormals: the hardware widening then gives f16_to_f32_ftz's bits for
+// every finite f16 value (a signalling NaN comes out quiet).  f32
+// arithmetic keeps its own mode (bits 5:4).
+constexpr int kHwregModeF16F64Denorm = 1 | (6 << 6) | ((2 - 1) << 11);
+
 // The same bits without branches (for loops that convert many values per
 // step): exponent and mantissa move up 13 bits and the exponent is rebiased
 // by 112 (<< 23 = 0x38000000), once more for Inf/NaN (31 -> 255), and

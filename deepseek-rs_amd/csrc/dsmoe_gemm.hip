@@ -1100,11 +1100,6 @@ extern "C" __global__ __launch_bounds__(64 * kQwWaves) void dsmoe_q80_wide_swigl
 // element 8 experts.
 // grid = ceil(E / 8) * ceil(T / 12), 256 threads.
 // ---------------------------------------------------------------------------
-namespace {
-// s_setreg operand for MODE bits 7:6 (the f16 / f64 denormal mode): hwreg id
-// 1, offset 6, size 2
-constexpr int kHwregModeF16F64Denorm = 1 | (6 << 6) | ((2 - 1) << 11);
-}  // namespace
 
 // NE experts x NT tokens per workgroup (NE * NT a multiple of 4): 8 x 12 for
 // large batches (165 registers: three waves per SIMD, where 8 x 16 tiles

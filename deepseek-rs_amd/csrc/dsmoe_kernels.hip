@@ -252,6 +252,12 @@ template <bool kCoh>
 __device__ __forceinline__ void role_router_logits(const RouterLogitsArgs& a, int bx, uint8_t* smem) {
   const int row = bx % a.E, t0 = (bx / a.E) * 8, tx = threadIdx.x;
   const int nt = min(8, a.T - t0);
+  // f16 input denormals flushed for this wave (it runs no other role): the
+  // hardware widening of the weights is then the reference's conversion, a
+  // signed zero for every subnormal (the value only enters a multiply, so a
+  // quieted signalling NaN gives the same product bits)
+  __builtin_amdgcn_s_setreg(kHwregModeF16F64Denorm, 0);
+  auto widen = [](uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); };
   const int d = a.d;  // d % 256 == 0 checked on the host
   const int nb = d >> 8;
   float (*part)[256] = (float (*)[256])smem;
@@ -262,7 +268,7 @@ __device__ __forceinline__ void role_router_logits(const RouterLogitsArgs& a, in
     for (int t = 0; t < nt; t++) {
       const float* xr = a.x + (size_t)(t0 + t) * d + tx;
       float acc = 0.0f;
-      for (int j = 0; j < nb; j++) acc = acc + f16_to_f32_ftz(wr[256 * j]) * xr[256 * j];
+      for (int j = 0; j < nb; j++) acc = acc + widen(wr[256 * j]) * xr[256 * j];
       part[t][tx] = acc;
     }
   } else {
@@ -278,7 +284,7 @@ __device__ __forceinline__ void role_router_logits(const RouterLogitsArgs& a, in
   }
   float w[32];
 #pragma unroll
-  for (int j = 0; j < 32; j++) w[j] = f16_to_f32_ftz((uint16_t)wh[j]);
+  for (int j = 0; j < 32; j++) w[j] = widen((uint16_t)wh[j]);
   for (int t = 0; t < nt; t++) {
     if (t > 0) {
       const float* xr = a.x + (size_t)(t0 + t) * d + tx;
