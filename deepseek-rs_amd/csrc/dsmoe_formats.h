@@ -129,6 +129,8 @@ DSM_HD float f16_to_f32_ftz(uint16_t h) {
 // every finite f16 value (a signalling NaN comes out quiet).  f32
 // arithmetic keeps its own mode (bits 5:4).
 constexpr int kHwregModeF16F64Denorm = 1 | (6 << 6) | ((2 - 1) << 11);
+// The kernels' default for those bits: f16 / f64 denormals kept (in and out).
+constexpr int kModeF16F64Preserve = 3;
 
 // The same bits without branches (for loops that convert many values per
 // step): exponent and mantissa move up 13 bits and the exponent is rebiased

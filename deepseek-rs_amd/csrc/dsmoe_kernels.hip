@@ -899,7 +899,9 @@ __device__ __forceinline__ float iq2_blk_dot(const uint32_t* w, uint32_t sel, ui
     const int32_t sumi = pos - neg - neg;
     asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(bsum) : "v"(sumi), "v"(ls), "v"(bsum));
   }
-  const float xd = f16_to_f32_ftz((uint16_t)(w[0] >> dsh));
+  // the wave runs with f16 input denormals flushed (dsmoe_up_rows): the
+  // hardware widening is the reference's conversion
+  const float xd = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[0] >> dsh));
   return 0.125f * xd * yd * (float)bsum;
 }
 
@@ -1659,7 +1661,7 @@ __device__ __forceinline__ void role_q80_rows(const Q80MatvecArgs& a, int tile, 
       int32_t d = 0;
 #pragma unroll
       for (int k = 0; k < 8; k++) d = dot4(__builtin_amdgcn_perm(wb[i][k + 1], wb[i][k], sel), qv[k], d);
-      const float sc = f16_to_f32_ftz((uint16_t)(wb[i][0] >> dsh));
+      const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)(wb[i][0] >> dsh));  // flushed: MODE
       p += sc * s_xs[b] * (float)d;
     }
   }
@@ -1838,6 +1840,11 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_up_rows(const UpArgs a) 
   __shared__ int s_flag;
   const int n_gu = a.gu_tiles * a.gu_work;
   int w = blockIdx.x;
+  // f16 input denormals flushed while the rows are summed (the block scales'
+  // widening is then one conversion, subnormals to signed zeros as in the
+  // reference); restored before the mid quantization, whose f16 scales keep
+  // their subnormal values
+  __builtin_amdgcn_s_setreg(kHwregModeF16F64Denorm, 0);
   auto arrive = [&](uint32_t* c, uint32_t n, uint32_t target) {
     return stores_done_then(&s_flag, [&] {
       if (__hip_atomic_fetch_add(c, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + n != target) return false;
@@ -1849,6 +1856,7 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_up_rows(const UpArgs a) 
     const int tile = w % a.gu_tiles, pair = w / a.gu_tiles;
     if (a.fuse_midq) {
       role_gate_up_rows_any(a, tile, pair, smem);
+      __builtin_amdgcn_s_setreg(kHwregModeF16F64Denorm, kModeF16F64Preserve);
       const int nbI = a.gu.I >> 8, row0 = tile * 32, blk = row0 >> 8;
       const uint32_t n = (uint32_t)min(32, a.gu.I - row0), target = (uint32_t)min(256, a.gu.I - (blk << 8));
       if (arrive(a.mid_cnt + pair * nbI + blk, n, target) && threadIdx.x < 64) q8k_block_wave<true>(a.midq, pair * nbI + blk);
@@ -1874,6 +1882,7 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_up_rows(const UpArgs a) 
         __builtin_amdgcn_s_sleep(127);
       }
       role_q80_rows_any(a.sh_q80, tile, tok, smem);
+      __builtin_amdgcn_s_setreg(kHwregModeF16F64Denorm, kModeF16F64Preserve);
       if (a.fuse_midq) {
         const int Is = a.sh_q80.out_dim, RT = 4, ng = (Is + 255) >> 8, row0 = tile * RT, g = row0 >> 8;
         const uint32_t n = (uint32_t)min(RT, Is - row0), target = (uint32_t)min(256, Is - (g << 8));
@@ -1933,6 +1942,9 @@ extern "C" __global__ __launch_bounds__(256) void dsmoe_dn_rows(const DnArgs a) 
   extern __shared__ __align__(16) uint8_t smem[];
   const int n_dn = a.dn_tiles * a.dn_work;
   int w = blockIdx.x;
+  // f16 input denormals flushed (the Q8_0 rows' scale widening; the launch
+  // writes no f16)
+  __builtin_amdgcn_s_setreg(kHwregModeF16F64Denorm, 0);
   if (w < n_dn) { role_down_rows_any(a.dn, w % a.dn_tiles, w / a.dn_tiles, smem); return; }
   w -= n_dn;
   if (w < a.sh_tiles * a.sh_work) {
